@@ -1,0 +1,390 @@
+// Greedy verify on gfx950: argmax over the vocabulary per verify row, accept
+// length against the drafted block, bonus token.
+//
+//  * lmhead_greedy_kernel: the lm_head matmul (same main loop as the dense
+//    qmm, full K per workgroup, 128 vocabulary rows per workgroup) whose
+//    epilogue rounds each logit to the activation dtype (the dtype the
+//    reference's logits carry), applies the optional Gemma softcap and the
+//    suppress mask, and reduces to a per-row (value, index) argmax key.  The
+//    logits never reach HBM unless the caller asks for them.
+//  * greedy_kernel: the same reduction over logits already in memory.
+//
+// Cross-workgroup reduction: a 64-bit key (monotone value bits << 32 |
+// ~index) per row, combined with atomicMax -- max is order-independent, so
+// the winner (largest value, then lowest index) is deterministic.  The last
+// workgroup to finish (atomic counter) turns the keys into tokens, computes
+// accept / bonus and clears the keys and the counter for the next call.
+#include <math.h>
+
+#include "dfmi_core.h"
+#include "dfmi_host.h"
+
+namespace dfmi {
+
+constexpr int kMaxGreedyRows = 32;
+
+struct GreedyOut {
+  unsigned long long* keys;  // [M] workspace, zero between calls
+  uint32_t* counter;         // workspace, zero between calls
+  uint32_t* posterior;       // [M]
+  int32_t* accept_len;       // [1] or null
+  uint32_t* bonus;           // [1] or null
+  const uint32_t* verify_ids;  // [M] or null
+  int M;
+};
+
+// Called by every workgroup after it has published its keys.  The last one
+// to arrive finalises.
+__device__ inline void greedy_finish(const GreedyOut& o, unsigned total_blocks) {
+  __shared__ int s_last;
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned prev = atomicAdd(o.counter, 1u);
+    s_last = (prev == total_blocks - 1) ? 1 : 0;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+  __shared__ uint32_t s_post[kMaxGreedyRows];
+  const int tid = threadIdx.x;
+  if (tid < o.M) {
+    const unsigned long long k =
+        __hip_atomic_load(&o.keys[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t tok = key_index(k);
+    s_post[tid] = tok;
+    o.posterior[tid] = tok;
+    __hip_atomic_store(&o.keys[tid], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    if (o.verify_ids != nullptr) {
+      int a = 0;
+      while (a + 1 < o.M && o.verify_ids[a + 1] == s_post[a]) ++a;
+      if (o.accept_len) o.accept_len[0] = a;
+      if (o.bonus) o.bonus[0] = s_post[a];
+    }
+    __hip_atomic_store(o.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+__device__ inline unsigned long long umax64(unsigned long long a, unsigned long long b) {
+  return a > b ? a : b;
+}
+
+// Max of a 64-bit key over the 16 lanes of each row of 16 (lanes l, l^1 .. l^8).
+__device__ inline unsigned long long max16(unsigned long long v) {
+#pragma unroll
+  for (int d = 1; d < 16; d <<= 1) v = umax64(v, __shfl_xor(v, d, 64));
+  return v;
+}
+
+__device__ inline unsigned long long max64(unsigned long long v) {
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) v = umax64(v, __shfl_xor(v, d, 64));
+  return v;
+}
+
+template <typename Tag>
+__device__ inline float round_t(float v) {
+  return Num<Tag>::h2f(Num<Tag>::f2h(v));
+}
+
+// logit value as the reference sees it: rounded to the dtype, optionally
+// softcapped with op-by-op rounding (target_gemma4.py:33-40).
+template <typename Tag>
+__device__ inline float logit_value(float acc, float capr) {
+  float v = round_t<Tag>(acc);
+  if (capr > 0.f) {
+    const float t1 = round_t<Tag>(v / capr);
+    const float t2 = round_t<Tag>(tanhf(t1));
+    v = round_t<Tag>(t2 * capr);
+  }
+  return v;
+}
+
+struct LmArgs {
+  const uint16_t* h;
+  const uint32_t* w;
+  const uint16_t* s;
+  const uint16_t* b;
+  const uint8_t* mask;
+  uint16_t* logits;  // [M, V] or null
+  float softcap;
+  int M, K, V;
+  int chunks;
+  int n_blocks;
+  GreedyOut out;
+};
+
+template <typename Tag, int GS, int MT, bool KFULL>
+__global__ __launch_bounds__(kThreads) void lmhead_greedy_kernel(LmArgs a) {
+  constexpr int NT = 2;
+  using C = Core<Tag, GS, MT, NT, KFULL>;
+  constexpr int NB = kWaves * 16 * NT;
+  __shared__ __attribute__((aligned(16))) char lds[C::LDS_BYTES];
+  __shared__ unsigned long long s_keys[kWaves][16 * MT];
+
+  const int nb = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t kw = (uint32_t)(a.K / 8);
+  const uint32_t kgrp = (uint32_t)(a.K / GS);
+
+  typename C::Stage st;
+#pragma unroll
+  for (int i = 0; i < C::SPT; ++i) {
+    const int slot = tid + kThreads * i;
+    int m, kk;
+    C::slot_geometry(slot, m, kk);
+    st.xoff[i] = m < a.M ? (int64_t)m * a.K : -1;
+    st.kk[i] = kk;
+    st.lds[i] = slot * 16;
+  }
+  const int col0 = nb * NB + wave * 16 * NT;
+  typename C::Rows r;
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int row = min(col0 + t * 16 + (lane & 15), a.V - 1);
+    r.wbase[t] = a.w;
+    r.sbase[t] = a.s;
+    r.bbase[t] = a.b;
+    r.woff[t] = (uint32_t)row * kw;
+    r.soff[t] = (uint32_t)row * kgrp;
+  }
+  f32x4 acc[NT][MT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[t][mt] = zero4();
+  C::run(a.h, st, r, a.K, 0, a.chunks, lds, acc);
+
+  const int kg = lane >> 4, col = lane & 15;
+  const float capr = a.softcap > 0.f ? round_t<Tag>(a.softcap) : 0.f;
+  const float neg = round_t<Tag>(-1e9f);
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int m = mt * 16 + 4 * kg + j;
+      unsigned long long best = 0ull;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const int n = col0 + t * 16 + col;
+        if (m < a.M && n < a.V) {
+          float v = logit_value<Tag>(acc[t][mt][j], capr);
+          if (a.logits) a.logits[(int64_t)m * a.V + n] = Num<Tag>::f2h(v);
+          if (a.mask && a.mask[n]) v = neg;
+          best = umax64(best, argmax_key(v, (uint32_t)n));
+        }
+      }
+      best = max16(best);
+      if (col == 0) s_keys[wave][mt * 16 + 4 * kg + j] = best;
+    }
+  }
+  __syncthreads();
+  if (tid < a.M) {
+    unsigned long long best = s_keys[0][tid];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) best = umax64(best, s_keys[w][tid]);
+    atomicMax(&a.out.keys[tid], best);
+  }
+  greedy_finish(a.out, (unsigned)a.n_blocks);
+}
+
+struct GreedyArgs {
+  const void* logits;
+  const uint8_t* mask;
+  int dtype;
+  int M, V;
+  int per_block;  // vocabulary entries per workgroup
+  GreedyOut out;
+};
+
+constexpr int kGreedyPerBlock = 4096;
+
+__global__ __launch_bounds__(kThreads) void greedy_kernel(GreedyArgs a) {
+  __shared__ unsigned long long s_keys[kWaves];
+  const int m = blockIdx.y;
+  const int v0 = blockIdx.x * a.per_block;
+  const int v1 = min(a.V, v0 + a.per_block);
+  const int tid = threadIdx.x;
+  float neg;
+  if (a.dtype == DFMI_BF16) neg = Num<BF16>::h2f(Num<BF16>::f2h(-1e9f));
+  else if (a.dtype == DFMI_F16) neg = Num<F16>::h2f(Num<F16>::f2h(-1e9f));
+  else neg = -1e9f;
+  unsigned long long best = 0ull;
+  const int64_t row = (int64_t)m * a.V;
+  for (int v = v0 + tid; v < v1; v += kThreads) {
+    float x;
+    if (a.dtype == DFMI_BF16) x = Num<BF16>::h2f(static_cast<const uint16_t*>(a.logits)[row + v]);
+    else if (a.dtype == DFMI_F16) x = Num<F16>::h2f(static_cast<const uint16_t*>(a.logits)[row + v]);
+    else x = static_cast<const float*>(a.logits)[row + v];
+    if (a.mask && a.mask[v]) x = neg;
+    best = umax64(best, argmax_key(x, (uint32_t)v));
+  }
+  best = max64(best);
+  if ((tid & 63) == 0) s_keys[tid >> 6] = best;
+  __syncthreads();
+  if (tid == 0) {
+    unsigned long long b = s_keys[0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) b = umax64(b, s_keys[w]);
+    atomicMax(&a.out.keys[m], b);
+  }
+  greedy_finish(a.out, gridDim.x * gridDim.y);
+}
+
+__global__ void accept_kernel(const uint32_t* drafted, const uint32_t* posterior, int64_t L,
+                              int32_t* out) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) {
+    int64_t a = 0;
+    while (a < L && drafted[a] == posterior[a]) ++a;
+    out[0] = (int32_t)a;
+  }
+}
+
+static size_t greedy_ws(int64_t M) { return 256 + round_up((size_t)M * 8u, 256); }
+
+static int bind_out(GreedyOut& o, void* ws, size_t ws_bytes, int64_t M, uint32_t* posterior,
+                    int32_t* accept_len, uint32_t* bonus, const uint32_t* verify_ids) {
+  if (!ws || ws_bytes < greedy_ws(M) || (reinterpret_cast<uintptr_t>(ws) & 7u)) {
+    set_error("greedy: workspace of %zu bytes (8-byte aligned) required, got %zu",
+              greedy_ws(M), ws_bytes);
+    return DFMI_ENOSPC;
+  }
+  o.counter = static_cast<uint32_t*>(ws);
+  o.keys = reinterpret_cast<unsigned long long*>(static_cast<char*>(ws) + 256);
+  o.posterior = posterior;
+  o.accept_len = accept_len;
+  o.bonus = bonus;
+  o.verify_ids = verify_ids;
+  o.M = (int)M;
+  return DFMI_OK;
+}
+
+template <typename Tag, int GS, int MT>
+static void launch_lm(bool kfull, int blocks, hipStream_t st, const LmArgs& a) {
+  if (kfull)
+    hipLaunchKernelGGL((lmhead_greedy_kernel<Tag, GS, MT, true>), dim3(blocks), dim3(kThreads), 0,
+                       st, a);
+  else
+    hipLaunchKernelGGL((lmhead_greedy_kernel<Tag, GS, MT, false>), dim3(blocks), dim3(kThreads),
+                       0, st, a);
+}
+
+template <typename Tag>
+static void launch_lm_tag(int gs, int mt, bool kfull, int blocks, hipStream_t st,
+                          const LmArgs& a) {
+  if (gs == 32) {
+    if (mt == 1) launch_lm<Tag, 32, 1>(kfull, blocks, st, a);
+    else launch_lm<Tag, 32, 2>(kfull, blocks, st, a);
+  } else if (gs == 64) {
+    if (mt == 1) launch_lm<Tag, 64, 1>(kfull, blocks, st, a);
+    else launch_lm<Tag, 64, 2>(kfull, blocks, st, a);
+  } else {
+    if (mt == 1) launch_lm<Tag, 128, 1>(kfull, blocks, st, a);
+    else launch_lm<Tag, 128, 2>(kfull, blocks, st, a);
+  }
+}
+
+}  // namespace dfmi
+
+using namespace dfmi;
+
+extern "C" size_t dfmi_greedy_workspace_bytes(int64_t M) { return greedy_ws(M); }
+extern "C" size_t dfmi_lmhead_workspace_bytes(int64_t M) { return greedy_ws(M); }
+
+extern "C" int dfmi_greedy_accept(const void* logits, int logits_dtype, const uint8_t* suppress_mask,
+                                  const uint32_t* verify_ids, int64_t M, int64_t V,
+                                  uint32_t* posterior, int32_t* accept_len, uint32_t* bonus,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
+  if (logits_dtype != DFMI_BF16 && logits_dtype != DFMI_F16 && logits_dtype != DFMI_F32) {
+    set_error("dfmi_greedy_accept: dtype %d unsupported", logits_dtype);
+    return DFMI_EINVAL;
+  }
+  if (M < 1 || M > kMaxGreedyRows || V < 1 || V >= (1ll << 31) || M * V >= (1ll << 40)) {
+    set_error("dfmi_greedy_accept: bad shape M=%lld V=%lld (1 <= M <= %d)", (long long)M,
+              (long long)V, kMaxGreedyRows);
+    return DFMI_EINVAL;
+  }
+  if (!logits || !posterior) {
+    set_error("dfmi_greedy_accept: null pointer");
+    return DFMI_EINVAL;
+  }
+  GreedyArgs a;
+  int rc = bind_out(a.out, workspace, workspace_bytes, M, posterior, accept_len, bonus, verify_ids);
+  if (rc != DFMI_OK) return rc;
+  a.logits = logits;
+  a.mask = suppress_mask;
+  a.dtype = logits_dtype;
+  a.M = (int)M;
+  a.V = (int)V;
+  a.per_block = kGreedyPerBlock;
+  const dim3 grid((unsigned)((V + kGreedyPerBlock - 1) / kGreedyPerBlock), (unsigned)M);
+  hipLaunchKernelGGL(greedy_kernel, grid, dim3(kThreads), 0, static_cast<hipStream_t>(stream), a);
+  return check_launch("dfmi_greedy_accept");
+}
+
+extern "C" int dfmi_lmhead_greedy_accept(const void* h, int h_dtype, const uint32_t* w_q,
+                                         const void* scales, const void* biases,
+                                         const uint8_t* suppress_mask, float softcap,
+                                         const uint32_t* verify_ids, int64_t M, int64_t K,
+                                         int64_t V, int group_size, int bits, uint32_t* posterior,
+                                         int32_t* accept_len, uint32_t* bonus, void* logits_out,
+                                         void* workspace, size_t workspace_bytes, void* stream) {
+  if (h_dtype != DFMI_BF16 && h_dtype != DFMI_F16) {
+    set_error("dfmi_lmhead_greedy_accept: dtype %d unsupported (bf16 or f16)", h_dtype);
+    return DFMI_EINVAL;
+  }
+  if (bits != 4 || (group_size != 32 && group_size != 64 && group_size != 128)) {
+    set_error("dfmi_lmhead_greedy_accept: bits=%d group_size=%d unsupported", bits, group_size);
+    return DFMI_EINVAL;
+  }
+  if (M < 1 || M > kMaxGreedyRows || V < 1 || K < 32 || K % 32 || K % group_size ||
+      V >= (1ll << 31) || K >= (1ll << 31) || V * (K / 8) > 0xFFFFFFFFll) {
+    set_error("dfmi_lmhead_greedy_accept: bad shape M=%lld K=%lld V=%lld", (long long)M,
+              (long long)K, (long long)V);
+    return DFMI_EINVAL;
+  }
+  if (!h || !w_q || !scales || !biases || !posterior) {
+    set_error("dfmi_lmhead_greedy_accept: null pointer");
+    return DFMI_EINVAL;
+  }
+  if (!aligned16(h) || !aligned16(w_q) || !aligned16(scales) || !aligned16(biases)) {
+    set_error("dfmi_lmhead_greedy_accept: h, w_q, scales and biases must be 16-byte aligned");
+    return DFMI_EINVAL;
+  }
+  LmArgs a;
+  int rc = bind_out(a.out, workspace, workspace_bytes, M, posterior, accept_len, bonus, verify_ids);
+  if (rc != DFMI_OK) return rc;
+  a.h = static_cast<const uint16_t*>(h);
+  a.w = w_q;
+  a.s = static_cast<const uint16_t*>(scales);
+  a.b = static_cast<const uint16_t*>(biases);
+  a.mask = suppress_mask;
+  a.logits = static_cast<uint16_t*>(logits_out);
+  a.softcap = softcap;
+  a.M = (int)M;
+  a.K = (int)K;
+  a.V = (int)V;
+  a.chunks = (int)((K + kChunkK - 1) / kChunkK);
+  const int nb_cols = kWaves * 16 * 2;
+  a.n_blocks = (int)((V + nb_cols - 1) / nb_cols);
+  const bool kfull = (K % kChunkK) == 0;
+  const int mt = M <= 16 ? 1 : 2;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (h_dtype == DFMI_BF16) launch_lm_tag<BF16>(group_size, mt, kfull, a.n_blocks, st, a);
+  else launch_lm_tag<F16>(group_size, mt, kfull, a.n_blocks, st, a);
+  return check_launch("dfmi_lmhead_greedy_accept");
+}
+
+extern "C" int dfmi_match_acceptance_length(const uint32_t* drafted, const uint32_t* posterior,
+                                            int64_t L, int32_t* out, void* stream) {
+  if (L < 0 || !out || (L > 0 && (!drafted || !posterior))) {
+    set_error("dfmi_match_acceptance_length: bad arguments");
+    return DFMI_EINVAL;
+  }
+  hipLaunchKernelGGL(accept_kernel, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream),
+                     drafted, posterior, L, out);
+  return check_launch("dfmi_match_acceptance_length");
+}

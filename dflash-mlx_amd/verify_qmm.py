@@ -1,0 +1,198 @@
+"""Verify-path quantized matmul with the reference's call surface.
+
+Mirrors dflash_mlx/verify_qmm.py: ``is_enabled`` (15-16), the variant
+predicates (21-51), ``_should_use_verify`` (886-903) and ``verify_matmul``
+(905-1022).  Every route -- the M=16 K-templated variants, the mma2big /
+mma2big_pipe variants, the M=4 k-split variant and the "stock" fallback that
+the reference hands to ``mx.quantized_matmul`` -- runs the same hand-written
+gfx950 kernel family in libdfmi.so (``dfmi_qmm_affine``).  The route only
+selects the launch shape: the reference's ``K_PARTS`` becomes the number of
+workgroups that split K (``DFLASH_VERIFY_QMM_KPARTS`` keeps its meaning), the
+others use the automatic shape.  All shapes compute the same sums in fp32 and
+differ only in fp32 summation order.
+
+Tensors: ``x`` bf16/f16 ``[..., K]`` on the GPU; ``w`` int32/uint32 words
+``[N, K*bits/32]``; ``scales``/``biases`` ``[N, K/group_size]`` in x's dtype.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from typing import Optional
+
+import torch
+
+from . import _lib, _runtime
+from .internal_debug import (
+    verify_qmm_enabled as _debug_verify_qmm_enabled,
+    verify_qmm_kparts as _debug_verify_qmm_kparts,
+    verify_qmm_variant as _debug_verify_qmm_variant,
+)
+
+_KERNEL_DTYPES = (torch.bfloat16, torch.float16)
+
+
+def is_enabled() -> bool:
+    return _debug_verify_qmm_enabled()
+
+
+def _variant() -> str:
+    return _debug_verify_qmm_variant()
+
+
+def _auto_variant(K: int, N: int) -> tuple[str, int]:
+    """dflash_mlx/verify_qmm.py:21-24."""
+    if K >= 8192 or N <= 8192:
+        return ("mma2big_pipe", 8)
+    return ("mma2big", 1)
+
+
+def _m4_ksplit_np_shape(K: int, N: int, bits: int) -> bool:
+    """dflash_mlx/verify_qmm.py:28-29."""
+    return int(bits) == 4 and int(N) % 4 == 0 and int(K) % 32 == 0
+
+
+def _m4_ksplit_np_kparts(N: int) -> int:
+    """dflash_mlx/verify_qmm.py:31-32."""
+    return 2 if int(N) >= 4096 else 4
+
+
+def _m16_ktmpl_variant(K: int, N: int, bits: int) -> Optional[str]:
+    """dflash_mlx/verify_qmm.py:34-41."""
+    if int(bits) != 4:
+        return None
+    if int(K) % 256 != 0 or int(N) % 16 != 0:
+        return None
+    if int(K) >= 8192 or int(N) <= 5120:
+        return "combo_ktmpl"
+    return "super_tree_fp16_ktmpl"
+
+
+def _resolve_m16_ktmpl_variant(K: int, N: int, bits: int,
+                               variant: Optional[str] = None) -> Optional[str]:
+    """dflash_mlx/verify_qmm.py:43-51."""
+    if int(bits) != 4 or int(K) % 256 != 0 or int(N) % 16 != 0:
+        return None
+    selected = _variant() if variant is None else str(variant)
+    if selected == "auto":
+        return _m16_ktmpl_variant(K, N, bits)
+    if selected in ("combo_ktmpl", "super_tree_fp16_ktmpl"):
+        return selected
+    return None
+
+
+def _tuning(k_splits: int = 0, tiles_per_wave: int = 0):
+    if not k_splits and not tiles_per_wave:
+        return None
+    return _lib.QmmTuning(int(tiles_per_wave), int(k_splits))
+
+
+def qmm_launch(x2: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+               N: int, group_size: int, bits: int, tuning=None,
+               out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """One ``dfmi_qmm_affine`` launch on the current stream: ``[M, K] -> [M, N]``."""
+    lib = _lib.load()
+    M, K = int(x2.shape[0]), int(x2.shape[1])
+    dev = x2.device
+    y = out if out is not None else torch.empty((M, N), dtype=x2.dtype, device=dev)
+    tptr = ctypes.byref(tuning) if tuning is not None else None
+    need = int(lib.dfmi_qmm_workspace_bytes_ex(M, K, N, int(group_size), int(bits), tptr))
+    ws, ws_bytes = _runtime.workspace(dev, need) if need else (0, 0)
+    status = lib.dfmi_qmm_affine_ex(
+        x2.data_ptr(), _runtime.dtype_code(x2.dtype), w.data_ptr(), scales.data_ptr(),
+        biases.data_ptr(), y.data_ptr(), M, K, N, int(group_size), int(bits),
+        ws, ws_bytes, tptr, _runtime.stream_ptr(dev))
+    _lib.check(status, "dfmi_qmm_affine")
+    return y
+
+
+def _prepare(x, w, scales, biases):
+    for t, name in ((x, "x"), (w, "w"), (scales, "scales"), (biases, "biases")):
+        _runtime.require_device(t, name)
+    if scales.dtype != x.dtype or biases is None or biases.dtype != x.dtype:
+        raise _lib.DfmiUnsupported(
+            _lib.DFMI_EINVAL, "scales and biases must exist and share x's dtype")
+    K = int(x.shape[-1])
+    M = math.prod(int(d) for d in x.shape[:-1])
+    x2 = _runtime.aligned_contiguous(x.reshape(M, K))
+    return (x2, _runtime.weight_words(w), _runtime.aligned_contiguous(scales),
+            _runtime.aligned_contiguous(biases), M, K)
+
+
+def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
+                     biases: torch.Tensor, *, transpose: bool = True, group_size: int = 64,
+                     bits: int = 4, mode: str = "affine", tuning=None) -> torch.Tensor:
+    """The "stock" quantized matmul of this framework (the role
+    ``mx.quantized_matmul`` plays for the reference): ``x . dequant(w)^T``.
+
+    Raises :class:`_lib.DfmiUnsupported` for what the kernels do not cover
+    (transpose=False, bits != 4, non-affine modes, fp32 activations).
+    """
+    if not transpose or mode != "affine":
+        raise _lib.DfmiUnsupported(_lib.DFMI_EINVAL,
+                                   "only transpose=True affine quantization is implemented")
+    if x.dtype not in _KERNEL_DTYPES:
+        raise _lib.DfmiUnsupported(_lib.DFMI_EINVAL, f"x dtype {x.dtype} unsupported")
+    x2, wq, s, b, M, K = _prepare(x, w, scales, biases)
+    N = int(wq.shape[0])
+    y = qmm_launch(x2, wq, s, b, N, group_size, bits, tuning)
+    return y.reshape(*x.shape[:-1], N)
+
+
+def _should_use_verify(x: torch.Tensor, group_size: int, bits: int, transpose: bool) -> bool:
+    """dflash_mlx/verify_qmm.py:886-903."""
+    if not is_enabled():
+        return False
+    if bits not in (4, 8) or group_size not in (32, 64, 128):
+        return False
+    if x.dtype not in _KERNEL_DTYPES:
+        return False
+    if not transpose:
+        return False
+    m = math.prod(int(d) for d in x.shape[:-1])
+    return m in (4, 16)
+
+
+def verify_route(M: int, K: int, N: int, bits: int,
+                 variant: Optional[str] = None) -> tuple[str, object]:
+    """Route of ``verify_matmul`` for an enabled M in {4, 16} call
+    (dflash_mlx/verify_qmm.py:933-1022): ``(name, tuning)``; name "stock"
+    means the reference would fall back to mx.quantized_matmul."""
+    if M == 4:
+        if not _m4_ksplit_np_shape(K, N, bits):
+            return "stock", None
+        return "m4_ksplit_np", None
+    selected = _variant() if variant is None else variant
+    ktmpl = _resolve_m16_ktmpl_variant(K, N, bits, selected)
+    if ktmpl is not None:
+        return ktmpl, None
+    auto_kp = None
+    if selected == "auto":
+        selected, auto_kp = _auto_variant(K, N)
+    k_parts = auto_kp if auto_kp is not None else _debug_verify_qmm_kparts(4)
+    if selected == "mma2big_pipe":
+        if N % 32 != 0 or k_parts <= 0 or K % (32 * k_parts) != 0:
+            return "stock", None
+        return "mma2big_pipe", _tuning(k_splits=k_parts)
+    if N % 32 != 0 or K % 32 != 0:
+        return "stock", None
+    return "mma2big", _tuning(k_splits=1)
+
+
+def verify_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
+                  biases: torch.Tensor, *, transpose: bool = True, group_size: int = 64,
+                  bits: int = 4) -> torch.Tensor:
+    """dflash_mlx/verify_qmm.py:905-1022 -- verify kernels for M in {4, 16}
+    when ``DFLASH_VERIFY_QMM=1``, else the stock quantized matmul."""
+    if not _should_use_verify(x, group_size, bits, transpose):
+        return quantized_matmul(x, w, scales, biases, transpose=transpose,
+                                group_size=group_size, bits=bits)
+    x2, wq, s, b, M, K = _prepare(x, w, scales, biases)
+    N = int(wq.shape[0])
+    route, tuning = verify_route(M, K, N, bits)
+    if route == "stock":
+        return quantized_matmul(x, w, scales, biases, transpose=transpose,
+                                group_size=group_size, bits=bits)
+    y = qmm_launch(x2, wq, s, b, N, group_size, bits, tuning)
+    return y.reshape(*x.shape[:-1], N)

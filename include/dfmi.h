@@ -1,0 +1,175 @@
+/*
+ * dfmi -- MI355X (gfx950) kernels for the dflash-mlx target-verify hot path.
+ *
+ * C ABI of libdfmi.so.  Plain pointers and sizes only: every pointer argument
+ * marked "device" is HIP device memory; `stream` is a hipStream_t (NULL = the
+ * null stream).  All launches are stream-ordered and asynchronous; a return of
+ * DFMI_OK means the work was enqueued.  No function allocates or frees device
+ * memory and none keeps a pointer past its return.  Functions are reentrant;
+ * the only process state is the thread-local error string.
+ *
+ * Packed-weight layout (the bytes dflash-mlx and MLX hand to the kernels,
+ * dflash_mlx/verify_qmm.py:97-115): w_q uint32 [N, K*bits/32] row-major,
+ * word j of row n holding k = j*(32/bits) .. , the first k in the lowest
+ * bits; scales and biases [N, K/group_size] in the activation dtype.
+ * Dequantised weight: w[n,k] = q[n,k]*scales[n,k/gs] + biases[n,k/gs].
+ *
+ * Workspaces: functions taking (workspace, workspace_bytes) need a device
+ * buffer of at least the size their *_workspace_bytes query returns.  The
+ * buffer must be zero-filled once when it is created; the kernels leave every
+ * counter and key they use back at zero when they finish, so one workspace
+ * serves any sequence of calls on ONE stream.  Calls that overlap in time
+ * (different streams) must not share a workspace, and the qmm family and the
+ * greedy family (greedy / lm_head) each need their own: each lays out its own
+ * counters (the qmm workspace starts with a fixed 64 KiB counter region).
+ */
+#ifndef DFMI_H
+#define DFMI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. */
+#define DFMI_OK 0
+#define DFMI_EINVAL (-1)   /* unsupported shape / dtype / alignment: caller falls back */
+#define DFMI_ELAUNCH (-2)  /* HIP launch error */
+#define DFMI_ENOSPC (-3)   /* workspace too small */
+
+/* Activation / scale dtypes. */
+#define DFMI_BF16 0
+#define DFMI_F16 1
+#define DFMI_F32 2
+
+/* Library version string and the message of the last failed call on this thread. */
+const char *dfmi_version(void);
+const char *dfmi_last_error(void);
+
+/* Optional launch-shape override for the affine qmm (tuning sweeps).  Zero
+ * fields mean "automatic".  tiles_per_wave: 16-row weight tiles per wavefront
+ * (1 or 2); k_splits: workgroups sharing one output block along K. */
+typedef struct dfmi_qmm_tuning {
+  int tiles_per_wave;
+  int k_splits;
+} dfmi_qmm_tuning;
+
+/*
+ * y[M, N] = x[M, K] . dequant(W)^T  (affine, transpose=True).
+ *
+ * Replaces the reference's M=16 / M=4 verify kernels AND the stock
+ * mx.quantized_matmul they fall back to:
+ *   dflash_mlx/verify_qmm.py:905-1022  verify_matmul (combo_ktmpl,
+ *     super_tree_fp16_ktmpl, mma2big, mma2big_pipe, m4_ksplit_np launches at
+ *     941-949, 961-973, 982-1002, 1009-1022)
+ *   dflash_mlx/verify_linear.py:166-175, 190-211, 223-232  per-module _run
+ *   mx.quantized_matmul(x, w, scales, biases, transpose=True, group_size, bits)
+ *     (verify_qmm.py:915-919 and every fallback site)
+ * x, scales, biases: dtype x_dtype (DFMI_BF16 or DFMI_F16); y: same dtype.
+ * Supported: bits == 4, group_size in {32, 64, 128}, K % 32 == 0,
+ * K % group_size == 0, any M >= 1, any N >= 1; 16-byte aligned x / w_q /
+ * scales / biases.  fp32 accumulation, output rounded to nearest even.
+ * Anything else returns DFMI_EINVAL without launching.
+ */
+int dfmi_qmm_affine(const void *x, int x_dtype, const uint32_t *w_q, const void *scales,
+                    const void *biases, void *y, int64_t M, int64_t K, int64_t N,
+                    int group_size, int bits, void *workspace, size_t workspace_bytes,
+                    void *stream);
+int dfmi_qmm_affine_ex(const void *x, int x_dtype, const uint32_t *w_q, const void *scales,
+                       const void *biases, void *y, int64_t M, int64_t K, int64_t N,
+                       int group_size, int bits, void *workspace, size_t workspace_bytes,
+                       const dfmi_qmm_tuning *tuning, void *stream);
+size_t dfmi_qmm_workspace_bytes(int64_t M, int64_t K, int64_t N, int group_size, int bits);
+size_t dfmi_qmm_workspace_bytes_ex(int64_t M, int64_t K, int64_t N, int group_size, int bits,
+                                   const dfmi_qmm_tuning *tuning);
+
+/*
+ * Routed-expert matmul: for each pair p < P,
+ *   y[p, N] = x[lhs_rows[p], K] . dequant(W[rhs_experts[p]])^T
+ * with w_q [E, N, K*bits/32], scales / biases [E, N, K/gs].
+ * Replaces mx.gather_qmm(x, w, scales, biases, rhs_indices=..., transpose=True,
+ * group_size, bits, sorted_indices=...) as called by mlx-lm's
+ * QuantizedSwitchLinear (reached from dflash_mlx/engine/target_qwen_gdn.py:865,874),
+ * with the lhs broadcast resolved to explicit row ids.  lhs_rows may be NULL
+ * (row p for pair p).  Pair order is free (sorted or not); results are
+ * per pair.  Expert ids outside [0, E) and row ids outside [0, x_rows) give
+ * DFMI_EINVAL (checked on the device: the pair's output row is filled with NaN
+ * and the call still returns DFMI_OK -- validate on the host when it matters).
+ */
+int dfmi_gather_qmm_affine(const void *x, int x_dtype, int64_t x_rows, const uint32_t *w_q,
+                           const void *scales, const void *biases, const int32_t *lhs_rows,
+                           const int32_t *rhs_experts, void *y, int64_t P, int64_t K, int64_t N,
+                           int64_t E, int group_size, int bits, void *stream);
+
+/*
+ * SwitchGLU front half, fused: for each pair p,
+ *   h[p, N] = silu(gate_p) * up_p,  gate_p = rnd(x_p . dequant(Wg[e])^T),
+ *   up_p = rnd(x_p . dequant(Wu[e])^T)   (rnd = round to x_dtype)
+ * i.e. mlx-lm SwitchGLU's gate_proj / up_proj gather_qmm pair plus its
+ * SwiGLU activation, one weight pass.  Same index conventions as above.
+ */
+int dfmi_gather_qmm_swiglu(const void *x, int x_dtype, int64_t x_rows,
+                           const uint32_t *wg_q, const void *g_scales, const void *g_biases,
+                           const uint32_t *wu_q, const void *u_scales, const void *u_biases,
+                           const int32_t *lhs_rows, const int32_t *rhs_experts, void *h,
+                           int64_t P, int64_t K, int64_t N, int64_t E, int group_size, int bits,
+                           void *stream);
+
+/*
+ * Weighted sum over each token's top-k expert outputs (the Qwen MoE block's
+ * `(y * scores[..., None]).sum(axis=-2)`):
+ *   out[t, D] = rnd(sum_j scores[t, j] * y[t*k + j, D])   (fp32 accumulate)
+ * y and out in y_dtype; scores fp32 [T, k].
+ */
+int dfmi_moe_combine(const void *y, int y_dtype, const float *scores, void *out, int64_t T,
+                     int64_t k, int64_t D, void *stream);
+
+/*
+ * Greedy verify over given logits: posterior[m] = argmax_v masked(logits[m, v])
+ * with masked ids set to dtype(-1e9) (dflash_mlx/engine/sampling.py:48-55),
+ * lowest index on ties, NaN never selected unless the row is all NaN.
+ * When verify_ids != NULL (M >= 1):
+ *   accept_len[0] = match_acceptance_length(verify_ids[1:], posterior[:-1])
+ *     (dflash_mlx/engine/acceptance.py:9-16, engine/spec_epoch.py:2070-2072)
+ *   bonus[0] = posterior[accept_len]            (engine/spec_epoch.py:2129)
+ * suppress_mask: uint8 [V] (nonzero = suppressed) or NULL.
+ * logits dtype: DFMI_BF16, DFMI_F16 or DFMI_F32.
+ */
+int dfmi_greedy_accept(const void *logits, int logits_dtype, const uint8_t *suppress_mask,
+                       const uint32_t *verify_ids, int64_t M, int64_t V, uint32_t *posterior,
+                       int32_t *accept_len, uint32_t *bonus, void *workspace,
+                       size_t workspace_bytes, void *stream);
+size_t dfmi_greedy_workspace_bytes(int64_t M);
+
+/*
+ * Fused lm_head + greedy + accept: the logits rnd(h . dequant(W_lm)^T)
+ * (optionally Gemma-softcapped: rnd(rnd(tanh(rnd(l / cap))) * cap), cap > 0)
+ * are reduced to the per-row argmax inside the matmul epilogue and never
+ * written unless logits_out != NULL.  Replaces the stock lm_head
+ * (dflash_mlx/engine/target_qwen_gdn.py:774-778, engine/target_gemma4.py:336-355)
+ * followed by greedy_tokens_with_mask and match_acceptance_length
+ * (engine/spec_epoch.py:2067-2072, 2129).  Outputs as dfmi_greedy_accept.
+ * M <= 32.
+ */
+int dfmi_lmhead_greedy_accept(const void *h, int h_dtype, const uint32_t *w_q, const void *scales,
+                              const void *biases, const uint8_t *suppress_mask, float softcap,
+                              const uint32_t *verify_ids, int64_t M, int64_t K, int64_t V,
+                              int group_size, int bits, uint32_t *posterior, int32_t *accept_len,
+                              uint32_t *bonus, void *logits_out, void *workspace,
+                              size_t workspace_bytes, void *stream);
+size_t dfmi_lmhead_workspace_bytes(int64_t M);
+
+/*
+ * match_acceptance_length on device arrays (dflash_mlx/engine/acceptance.py:9-16):
+ * out[0] = length of the longest prefix with drafted[i] == posterior[i]; 0 for L == 0.
+ */
+int dfmi_match_acceptance_length(const uint32_t *drafted, const uint32_t *posterior, int64_t L,
+                                 int32_t *out, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DFMI_H */

@@ -1,0 +1,164 @@
+"""GPU parity of the dense affine qmm (libdfmi ``dfmi_qmm_affine``) against the
+CPU oracle, on seeded inputs.  Tolerance (written here, from the verify path's
+contract): max|y - y_ref| / (max|y_ref| + 1e-3) <= 1e-2 (the reference's own
+metric, tests/test_verify_qmm_parity.py:69-70, at half the reference's 2e-2),
+plus an elementwise bound of 2 output ulps around the exact result."""
+
+from __future__ import annotations
+
+import json
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from tests.conftest import from_dev, make_qmm_case, to_dev
+
+pytestmark = pytest.mark.gpu
+
+GOLD = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "reference_cases.json")))
+REL_TOL = 1e-2
+
+
+def _run(dev, x, w_q, s, b, gs, dtype="bf16", tuning=None, via="stock", monkeypatch=None):
+    import torch
+
+    from dflash_mlx_amd import verify_qmm as vq
+
+    xt, st, bt = to_dev(x, dtype, dev), to_dev(s, dtype, dev), to_dev(b, dtype, dev)
+    wt = to_dev(w_q, "u32", dev)
+    if via == "verify":
+        y = vq.verify_matmul(xt, wt, st, bt, transpose=True, group_size=gs, bits=4)
+    else:
+        y = vq.quantized_matmul(xt, wt, st, bt, transpose=True, group_size=gs, bits=4,
+                                tuning=tuning)
+    torch.cuda.synchronize()
+    return from_dev(y, dtype)
+
+
+def _check(got, x, w_q, s, b, gs, dtype="bf16"):
+    ref = oracle.quantized_matmul(x, w_q, s, b, group_size=gs, bits=4, dtype=dtype)
+    g = oracle.to_f32(got, dtype).astype(np.float64)
+    max_abs, max_rel = oracle.parity_metrics(g, ref)
+    assert g.shape == ref.shape
+    assert np.all(np.isfinite(g))
+    assert max_rel <= REL_TOL, f"max_rel={max_rel:.3g} max_abs={max_abs:.3g}"
+    ulp = 2.0 ** -8 if dtype == "bf16" else 2.0 ** -11
+    bound = 2 * ulp * np.abs(ref) + 1e-4 * np.abs(ref).max()
+    assert np.all(np.abs(g - ref) <= bound), "elementwise bound"
+    return max_rel
+
+
+def test_config1_single_call(dev):
+    # [16,4096] x [4096,4096], x ~ N(0,1), W ~ N(0,0.02), int4 gs64
+    x, w_q, s, b = make_qmm_case(16, 4096, 4096, 64, seed=1)
+    _check(_run(dev, x, w_q, s, b, 64), x, w_q, s, b, 64)
+
+
+@pytest.mark.parametrize("K,N", [(4096, 4096), (4096, 1024), (4096, 12288), (12288, 4096),
+                                 (5120, 5120), (5120, 1024), (5120, 17408), (17408, 5120)])
+def test_baseline_layer_shapes_m16(dev, K, N):
+    x, w_q, s, b = make_qmm_case(16, K, N, 64, seed=K + N)
+    _check(_run(dev, x, w_q, s, b, 64), x, w_q, s, b, 64)
+
+
+@pytest.mark.parametrize("M", [1, 4, 8, 12, 15, 17, 24, 32, 48, 80])
+def test_m_sweep(dev, M):
+    x, w_q, s, b = make_qmm_case(M, 2048, 768, 64, seed=100 + M)
+    _check(_run(dev, x, w_q, s, b, 64), x, w_q, s, b, 64)
+
+
+@pytest.mark.parametrize("gs", [32, 64, 128])
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_group_sizes_and_dtypes(dev, gs, dtype):
+    x, w_q, s, b = make_qmm_case(16, 1536, 640, gs, dtype=dtype, seed=gs)
+    _check(_run(dev, x, w_q, s, b, gs, dtype), x, w_q, s, b, gs, dtype)
+
+
+@pytest.mark.parametrize("K,N", [(1088, 232), (448, 16), (128, 488), (96, 40), (2496, 72)])
+def test_ragged_k_and_n(dev, K, N):
+    # K not a multiple of 256 (partial last chunk), N not a multiple of 16.
+    x, w_q, s, b = make_qmm_case(16, K, N, 32, seed=K * 7 + N)
+    _check(_run(dev, x, w_q, s, b, 32), x, w_q, s, b, 32)
+
+
+@pytest.mark.parametrize("name,M,K,N", GOLD["random_shapes"])
+def test_reference_random_shapes(dev, name, M, K, N, monkeypatch):
+    # tests/test_verify_qmm_parity.py:32-42 shape list, through verify_matmul
+    monkeypatch.setenv("DFLASH_VERIFY_QMM", "1")
+    x, w_q, s, b = make_qmm_case(M, K, N, 64, seed=int(name[3:]))
+    _check(_run(dev, x, w_q, s, b, 64, via="verify"), x, w_q, s, b, 64)
+
+
+@pytest.mark.parametrize("name,M,K,N", GOLD["real_mlp_shapes"])
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_reference_real_mlp_shapes(dev, name, M, K, N, dtype, monkeypatch):
+    # tests/test_verify_qmm_parity.py:16-27, inputs N(0,1)/sqrt(K) as there (29-52)
+    monkeypatch.setenv("DFLASH_VERIFY_QMM", "1")
+    sc = 1.0 / np.sqrt(K)
+    x, w_q, s, b = make_qmm_case(M, K, N, 64, dtype=dtype, seed=N + M, x_std=sc, w_std=sc)
+    _check(_run(dev, x, w_q, s, b, 64, dtype, via="verify"), x, w_q, s, b, 64, dtype)
+
+
+def test_closed_form_exact(dev):
+    # scale 1/8, bias -1, sparse +-1 activations: every partial sum is a small
+    # dyadic number, exact in fp32 and in bf16, so the output must be bit-exact.
+    # Pins the nibble order, the activation permutation and the MFMA lane layout.
+    rng = np.random.default_rng(42)
+    M, K, N, gs = 16, 1024, 128, 64
+    q = rng.integers(0, 16, size=(N, K))
+    w_q = oracle.pack(q, 4)
+    s = oracle.f32_to_bf16_bits(np.full((N, K // gs), 0.125, np.float32))
+    b = oracle.f32_to_bf16_bits(np.full((N, K // gs), -1.0, np.float32))
+    xf = np.zeros((M, K), np.float32)
+    for m in range(M):
+        idx = rng.choice(K, size=6, replace=False)
+        xf[m, idx] = rng.choice([-1.0, 1.0], size=6)
+    x = oracle.f32_to_bf16_bits(xf)
+    want = oracle.quantized_matmul(x, w_q, s, b, group_size=gs, out_dtype="bf16")
+    for tuning in (None, (1, 1), (2, 4), (1, 4)):
+        got = _run(dev, x, w_q, s, b, gs, tuning=_tuning(tuning))
+        assert np.array_equal(got, want), f"tuning {tuning}"
+
+
+def _tuning(t):
+    if t is None:
+        return None
+    from dflash_mlx_amd import _lib
+
+    return _lib.QmmTuning(t[0], t[1])
+
+
+@pytest.mark.parametrize("tiles,splits", [(1, 1), (2, 1), (1, 2), (2, 3), (1, 8), (2, 16)])
+def test_launch_shapes_agree(dev, tiles, splits):
+    x, w_q, s, b = make_qmm_case(16, 4096, 2048, 64, seed=77)
+    got = _run(dev, x, w_q, s, b, 64, tuning=_tuning((tiles, splits)))
+    _check(got, x, w_q, s, b, 64)
+
+
+def test_deterministic_and_workspace_reuse(dev):
+    # The K-split reduction sums partials in split order, so repeated calls are
+    # bit-identical; interleaving other shapes must not disturb the counters.
+    x, w_q, s, b = make_qmm_case(16, 4096, 4096, 64, seed=5)
+    x2, w2, s2, b2 = make_qmm_case(16, 5120, 1024, 64, seed=6)
+    first = _run(dev, x, w_q, s, b, 64)
+    for _ in range(3):
+        _run(dev, x2, w2, s2, b2, 64)
+        assert np.array_equal(_run(dev, x, w_q, s, b, 64), first)
+
+
+def test_unsupported_raises(dev):
+    import torch
+
+    from dflash_mlx_amd import _lib
+    from dflash_mlx_amd import verify_qmm as vq
+
+    x = torch.zeros((16, 100), dtype=torch.bfloat16, device=dev)  # K % 32 != 0
+    w = torch.zeros((8, 100 // 8), dtype=torch.int32, device=dev)
+    s = torch.zeros((8, 2), dtype=torch.bfloat16, device=dev)
+    with pytest.raises(_lib.DfmiUnsupported):
+        vq.quantized_matmul(x, w, s, s, group_size=50, bits=4)
+    xf = torch.zeros((16, 64), dtype=torch.float32, device=dev)
+    with pytest.raises(_lib.DfmiUnsupported):
+        vq.quantized_matmul(xf, w[:, :8], s[:, :1], s[:, :1], group_size=64, bits=4)
