@@ -129,8 +129,8 @@ def run_sweep(args, torch, pkg):
     step_bytes = sum(alg_bytes(M, x.shape[1], w.shape[0]) for (x, w, _, _, _) in calls)
 
     tuning = None
-    if args.tiles or args.splits:
-        tuning = _lib.QmmTuning(args.tiles, args.splits)
+    if args.path or args.tiles or args.splits:
+        tuning = _lib.QmmTuning(args.path, args.tiles, args.splits, args.splits)
     # size the workspace before any capture
     need = 0
     lib = _lib.load()
@@ -217,6 +217,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="9b", choices=["9b", "27b"])
     ap.add_argument("--m", type=int, default=16)
+    ap.add_argument("--path", type=int, default=0, help="1 general kernel, 2 streaming kernel")
     ap.add_argument("--tiles", type=int, default=0)
     ap.add_argument("--splits", type=int, default=0)
     ap.add_argument("--no-graph", action="store_true")

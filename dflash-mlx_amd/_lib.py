@@ -29,7 +29,11 @@ _float = ctypes.c_float
 
 
 class QmmTuning(ctypes.Structure):
-    _fields_ = [("tiles_per_wave", ctypes.c_int), ("k_splits", ctypes.c_int)]
+    """dfmi_qmm_tuning: path (1 general, 2 streaming), tiles_per_wave,
+    waves_per_block (general kernel K split), k_splits (streaming kernel K
+    split across workgroups); 0 = automatic."""
+    _fields_ = [("path", ctypes.c_int), ("tiles_per_wave", ctypes.c_int),
+                ("waves_per_block", ctypes.c_int), ("k_splits", ctypes.c_int)]
 
 
 # name -> (restype, argtypes)

@@ -28,6 +28,9 @@ CFLAGS = [
     "-fPIC",
     "-Wall",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in VGPRs: the per-group scale FMAs read them directly
+    # instead of copying each accumulator out of an AGPR first.
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
 ]
 
 

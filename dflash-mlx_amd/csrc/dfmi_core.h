@@ -1,27 +1,32 @@
-// Main loop of every verify-path matmul: a workgroup of 4 wavefronts streams
-// the packed weights of 4*NT 16-row tiles over a range of K "chunks" (256 k
-// = 128 bytes of each int4 weight row), with the activations for the chunk
-// staged once per workgroup in LDS.
+// Main loop of every verify-path matmul.
+//
+// A workgroup owns NT 16-row weight tiles (16*NT output columns) and all M
+// rows of the activations (MT 16-row MFMA blocks).  Its W wavefronts split K:
+// wavefront w streams its share of the K "chunks" (256 k = 128 bytes of each
+// int4 weight row) for all NT tiles, and the W partial tiles are summed once
+// through LDS at the end.  There is no cross-workgroup reduction, hence no
+// device-scope fence and no atomic on the matmul path.
 //
 // Per chunk and wavefront lane (col = lane & 15, kg = lane >> 4):
 //   * weights: for each group g of the chunk the lane loads the WPL = gs/32
 //     consecutive words kg*WPL .. of that group (one dword / dwordx2 / dwordx4
 //     load), so the 4 lanes of one column cover the group and every
 //     16x16x32 MFMA stays inside one quantisation group;
-//   * the 8 activation fragments (16 rows x 256 k, pre-permuted to the
-//     nibble order of dequant_word4) come from LDS with ds_read_b128;
+//   * activations: the 8 fragments (16 rows x 256 k) straight from global
+//     memory (L2-resident: every workgroup reads the same x), used as MFMA
+//     operands in k order (dequant_word4 emits the weights in k order);
 //   * X[m, g] (group sums of the activations) come from MFMAs against an
 //     all-ones operand, which lands them in the layout the fp32 bias MFMA needs.
-// The next chunk's weights and activations are in flight while the current
-// one is computed (two register sets, two LDS buffers, one barrier per chunk).
+// Chunk c+1 is loaded (unconditionally: the index is clamped to the last
+// chunk, whose lines are then already in cache) before chunk c is computed,
+// so every wait in the loop is for loads issued one iteration earlier.
 #pragma once
 
 #include "dfmi_device.h"
 
 namespace dfmi {
 
-constexpr int kWaves = 4;
-constexpr int kThreads = kWaves * 64;
+constexpr int kMaxWaves = 8;
 constexpr int kChunkK = 256;
 
 template <typename Tag, int GS, int MT, int NT, bool KFULL>
@@ -30,55 +35,64 @@ struct Core {
   static constexpr int WPL = GS / 32;          // words per lane per group (1/2/4)
   static constexpr int FR = kChunkK / 32;      // 16x16x32 MFMA k-blocks per chunk (8)
   static constexpr int NBB = (GPC + 3) / 4;    // fp32 bias MFMAs per chunk and tile
-  static constexpr int SPT = MT * FR * 64 / kThreads;  // staging slots per thread
   static constexpr int SVEC = (GPC + 1) / 2;   // u32 registers for the chunk's scales
-  static constexpr int LDS_BUF = MT * FR * 64 * 16;    // bytes of one staged chunk
-  static constexpr int LDS_BYTES = 2 * LDS_BUF;
+  // LDS for the cross-wavefront reduction: [wave][t][mt][reg][lane] floats.
+  static constexpr int RED_FLOATS_PER_WAVE = NT * MT * 4 * 64;
+  static constexpr int LDS_BYTES = kMaxWaves * RED_FLOATS_PER_WAVE * 4;
   static_assert(GS == 32 || GS == 64 || GS == 128, "group size");
-  static_assert(SPT >= 1, "staging");
 
   struct Tile {
     uint32_t w[FR];    // packed words, group g word h at w[g*WPL + h]
     uint32_t s[SVEC];  // the chunk's GPC scales of this lane's row, packed pairs
-    uint32_t bq[NBB];  // raw 16-bit bias of group 4*bb + kg
-    uint32_t sq[NBB];  // raw 16-bit scale of group 4*bb + kg
+    uint32_t b[SVEC];  // the chunk's GPC biases of this lane's row, packed pairs
   };
 
-  // Per-thread staging description (fixed for the whole workgroup).
-  struct Stage {
-    int64_t xoff[SPT];  // element offset of the activation row start, -1 = zero row
-    int kk[SPT];        // k offset of the slot inside a chunk
-    int lds[SPT];       // byte offset of the slot inside a buffer
+  struct XFrag {
+    u32x4 v[MT][FR];  // activations of the chunk, fragment f = MFMA k-block f
   };
 
-  // Slot s (tid + 256*i) -> (mt, f, l) with MFMA fragment f of row block mt for
-  // lane l; row m = mt*16 + (l & 15); k offset g*GS + ((l>>4)*WPL + h)*8.
-  __device__ static inline void slot_geometry(int slot, int& m, int& kk) {
-    const int mt = slot / (FR * 64);
-    const int f = (slot / 64) % FR;
-    const int l = slot % 64;
-    const int g = f / WPL, h = f % WPL;
-    m = mt * 16 + (l & 15);
-    kk = g * GS + ((l >> 4) * WPL + h) * 8;
-  }
+  // Per-tile row addressing of this lane.
+  struct Rows {
+    const uint32_t* wbase[NT];
+    const uint16_t* sbase[NT];
+    const uint16_t* bbase[NT];
+    uint32_t woff[NT];  // word offset of this lane's row in tile t
+    uint32_t soff[NT];  // element offset of this lane's row in scales / biases
+  };
 
-  __device__ static inline void stage_load(const uint16_t* __restrict__ x, const Stage& st, int c,
-                                           int K, u32x4 (&v)[SPT]) {
+  // Activation rows of this lane: element offset of row mt*16 + (lane&15).
+  // Rows >= M point at a valid row instead: MFMA rows are independent, so a
+  // duplicated activation row only produces output rows that are never
+  // stored, and every load stays unconditional (a load under a divergent
+  // branch would force the compiler to wait for all outstanding loads).
+  struct XRows {
+    int64_t off[MT];
+  };
+
+  __device__ static inline XRows x_rows(int m_base, int M, int K, int lane) {
+    XRows xr;
 #pragma unroll
-    for (int i = 0; i < SPT; ++i) {
-      const int k = c * kChunkK + st.kk[i];
-      if (st.xoff[i] >= 0 && (KFULL || k < K)) {
-        v[i] = *reinterpret_cast<const u32x4*>(x + st.xoff[i] + k);
-      } else {
-        v[i] = u32x4{0u, 0u, 0u, 0u};
-      }
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = min(m_base + mt * 16 + (lane & 15), M - 1);
+      xr.off[mt] = (int64_t)m * K;
     }
+    return xr;
   }
 
-  __device__ static inline void stage_store(char* lds_buf, const Stage& st, const u32x4 (&v)[SPT]) {
+  __device__ static inline void load_x(XFrag& xf, const uint16_t* __restrict__ x,
+                                       const XRows& xr, int c, int K, int kg) {
 #pragma unroll
-    for (int i = 0; i < SPT; ++i) {
-      *reinterpret_cast<u32x4*>(lds_buf + st.lds[i]) = permute_x8(v[i]);
+    for (int f = 0; f < FR; ++f) {
+      const int g = f / WPL, h = f % WPL;
+      const int k = c * kChunkK + g * GS + (kg * WPL + h) * 8;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        if (KFULL || k < K) {
+          xf.v[mt][f] = *reinterpret_cast<const u32x4*>(x + xr.off[mt] + k);
+        } else {
+          xf.v[mt][f] = u32x4{0u, 0u, 0u, 0u};
+        }
+      }
     }
   }
 
@@ -106,49 +120,70 @@ struct Core {
     }
     const uint32_t so = soff + (uint32_t)(c * GPC);
     if constexpr (KFULL) {
-      const uint32_t* sp = reinterpret_cast<const uint32_t*>(sbase + so);
-      if constexpr (SVEC == 4) {
-        u32x4 v = *reinterpret_cast<const u32x4*>(sp);
-        t.s[0] = v.x; t.s[1] = v.y; t.s[2] = v.z; t.s[3] = v.w;
-      } else if constexpr (SVEC == 2) {
-        u32x2 v = *reinterpret_cast<const u32x2*>(sp);
-        t.s[0] = v.x; t.s[1] = v.y;
-      } else {
-        t.s[0] = sp[0];
-      }
+      load_vec(t.s, sbase + so);
+      load_vec(t.b, bbase + so);
     } else {
 #pragma unroll
       for (int j = 0; j < SVEC; ++j) {
-        uint32_t lo = 0u, hi = 0u;
-        if ((c * kChunkK + (2 * j) * GS) < K) lo = sbase[so + 2 * j];
-        if (2 * j + 1 < GPC && (c * kChunkK + (2 * j + 1) * GS) < K) hi = sbase[so + 2 * j + 1];
-        t.s[j] = lo | (hi << 16);
+        uint32_t slo = 0u, shi = 0u, blo = 0u, bhi = 0u;
+        if ((c * kChunkK + (2 * j) * GS) < K) {
+          slo = sbase[so + 2 * j];
+          blo = bbase[so + 2 * j];
+        }
+        if (2 * j + 1 < GPC && (c * kChunkK + (2 * j + 1) * GS) < K) {
+          shi = sbase[so + 2 * j + 1];
+          bhi = bbase[so + 2 * j + 1];
+        }
+        t.s[j] = slo | (shi << 16);
+        t.b[j] = blo | (bhi << 16);
       }
     }
-#pragma unroll
-    for (int bb = 0; bb < NBB; ++bb) {
-      const int gi = 4 * bb + kg;
-      const bool ok = gi < GPC && (KFULL || (c * kChunkK + gi * GS) < K);
-      t.bq[bb] = ok ? (uint32_t)bbase[so + gi] : 0u;
-      t.sq[bb] = ok ? (uint32_t)sbase[so + gi] : 0u;
+  }
+
+  // The chunk's GPC 16-bit values of one row (scales or biases) in SVEC registers.
+  __device__ static inline void load_vec(uint32_t (&dst)[SVEC], const uint16_t* __restrict__ p) {
+    const uint32_t* sp = reinterpret_cast<const uint32_t*>(p);
+    if constexpr (SVEC == 4) {
+      u32x4 v = *reinterpret_cast<const u32x4*>(sp);
+      dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;
+    } else if constexpr (SVEC == 2) {
+      u32x2 v = *reinterpret_cast<const u32x2*>(sp);
+      dst[0] = v.x; dst[1] = v.y;
+    } else {
+      dst[0] = sp[0];
     }
+  }
+
+  // 16-bit value of group 4*bb + kg (0 when the chunk has no such group).
+  // Bitwise selects only: a lane-dependent array index would be lowered to a
+  // scratch-memory round trip.
+  __device__ static inline uint32_t lane_group_value(const uint32_t (&v)[SVEC], int bb, int kg) {
+    uint32_t reg;
+    if constexpr (SVEC == 1) {
+      reg = v[0];
+    } else {
+      const uint32_t hi_mask = 0u - (uint32_t)((kg >> 1) & 1);
+      reg = (v[2 * bb + 1] & hi_mask) | (v[2 * bb] & ~hi_mask);
+    }
+    const uint32_t val = (reg >> ((kg & 1) * 16)) & 0xFFFFu;
+    return (4 * bb + kg < GPC) ? val : 0u;
+  }
+
+  __device__ static inline void load_chunk(XFrag& xf, Tile (&tl)[NT], const uint16_t* __restrict__ x,
+                                           const XRows& xr, const Rows& r, int c, int K, int kg) {
+    load_x(xf, x, xr, c, K, kg);
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+      load_tile(tl[t], r.wbase[t], r.sbase[t], r.bbase[t], r.woff[t], r.soff[t], c, K, kg);
   }
 
   __device__ static inline float scale_of(const Tile& t, int g) {
     return (g & 1) ? Num<Tag>::hi(t.s[g >> 1]) : Num<Tag>::lo(t.s[g >> 1]);
   }
 
-  // One chunk: activations from LDS, then every tile of this wavefront.
-  __device__ static inline void compute_chunk(const char* lds_buf, const Tile (&tl)[NT],
-                                              f32x4 (&acc)[NT][MT], int lane) {
-    const int kg = lane >> 4;
-    u32x4 a[MT][FR];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int f = 0; f < FR; ++f)
-        a[mt][f] = *reinterpret_cast<const u32x4*>(lds_buf + ((mt * FR + f) * 64 + lane) * 16);
-
+  __device__ static inline void compute_chunk(const XFrag& xf, const Tile (&tl)[NT],
+                                              f32x4 (&acc)[NT][MT], int kg, const DqConst& dq) {
+    const auto& a = xf.v;
     // Group sums of the activations: C = ONES . A^T puts X[m = lane&15, g] in every register.
     const u32x4 ones = u32x4{Num<Tag>::ONE2, Num<Tag>::ONE2, Num<Tag>::ONE2, Num<Tag>::ONE2};
     float xa[MT][NBB];
@@ -182,7 +217,7 @@ struct Core {
         for (int mt = 0; mt < MT; ++mt) p[mt] = zero4();
 #pragma unroll
         for (int h = 0; h < WPL; ++h) {
-          const u32x4 b = dequant_word4<Tag>(tl[t].w[g * WPL + h]);
+          const u32x4 b = dequant_word4<Tag>(tl[t].w[g * WPL + h], dq);
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) p[mt] = Num<Tag>::mma(a[mt][g * WPL + h], b, p[mt]);
         }
@@ -197,58 +232,91 @@ struct Core {
       }
 #pragma unroll
       for (int bb = 0; bb < NBB; ++bb) {
-        const float bq = __builtin_fmaf(-Num<Tag>::OFF, Num<Tag>::h2f(tl[t].sq[bb]),
-                                        Num<Tag>::h2f(tl[t].bq[bb]));
+        const float bq =
+            __builtin_fmaf(-Num<Tag>::OFF, Num<Tag>::h2f(lane_group_value(tl[t].s, bb, kg)),
+                           Num<Tag>::h2f(lane_group_value(tl[t].b, bb, kg)));
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) acc[t][mt] = mma_f32_16x16x4(xa[mt][bb], bq, acc[t][mt]);
       }
     }
   }
 
-  struct Rows {
-    const uint32_t* wbase[NT];
-    const uint16_t* sbase[NT];
-    const uint16_t* bbase[NT];
-    uint32_t woff[NT];  // word offset of this lane's row in tile t
-    uint32_t soff[NT];  // element offset of this lane's row in scales / biases
-  };
+  // Accumulate chunks [c0, c1) (c1 > c0) into acc (acc is not cleared here).
+  //
+  // Two register sets A/B; chunk c+1 is in flight while chunk c is computed.
+  // Only valid chunks are ever loaded (a redundant load would add a full
+  // memory round trip before the wavefront can retire), and every load sits
+  // in straight-line code: the steady-state loop runs while both of its
+  // prefetches are valid and the last two or three chunks are peeled, so the
+  // compiler can wait for exactly the older loads (a load behind a branch
+  // would make it wait for all of them, or sink the load into the branch).
+  // sched_barrier keeps the machine scheduler from sinking a prefetch below
+  // the compute it is meant to overlap.
+  __device__ static inline void run(const uint16_t* __restrict__ x, const XRows& xr,
+                                    const Rows& r, int K, int c0, int c1,
+                                    f32x4 (&acc)[NT][MT]) {
+    const int kg = (threadIdx.x & 63) >> 4;
+    const DqConst dq = dq_const<Tag>();
+    if constexpr (MT * NT > 1) {
+      // Larger register tiles: a single register set (two would spill).
+      for (int c = c0; c < c1; ++c) {
+        XFrag xf;
+        Tile tl[NT];
+        load_chunk(xf, tl, x, xr, r, c, K, kg);
+        compute_chunk(xf, tl, acc, kg, dq);
+      }
+      return;
+    }
+    XFrag xa, xb;
+    Tile ta[NT], tb[NT];
+    load_chunk(xa, ta, x, xr, r, c0, K, kg);
+    if (c1 - c0 == 1) {
+      compute_chunk(xa, ta, acc, kg, dq);
+      return;
+    }
+    load_chunk(xb, tb, x, xr, r, c0 + 1, K, kg);
+    __builtin_amdgcn_sched_barrier(0);
+    int c = c0;
+    for (; c + 3 < c1; c += 2) {
+      compute_chunk(xa, ta, acc, kg, dq);
+      load_chunk(xa, ta, x, xr, r, c + 2, K, kg);
+      __builtin_amdgcn_sched_barrier(0);
+      compute_chunk(xb, tb, acc, kg, dq);
+      load_chunk(xb, tb, x, xr, r, c + 3, K, kg);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (c1 - c == 3) {
+      compute_chunk(xa, ta, acc, kg, dq);
+      load_chunk(xa, ta, x, xr, r, c + 2, K, kg);
+      __builtin_amdgcn_sched_barrier(0);
+      compute_chunk(xb, tb, acc, kg, dq);
+      compute_chunk(xa, ta, acc, kg, dq);
+    } else {
+      compute_chunk(xa, ta, acc, kg, dq);
+      compute_chunk(xb, tb, acc, kg, dq);
+    }
+  }
 
-  __device__ static inline void load_tiles(Tile (&tl)[NT], const Rows& r, int c, int K, int kg) {
+  // Sum the wavefronts' partial tiles through LDS; afterwards thread e
+  // (e < RED_FLOATS_PER_WAVE, e = ((t*MT + mt)*4 + reg)*64 + lane) calls
+  // out(t, mt, reg, lane, value) for each element it owns.
+  template <typename Out>
+  __device__ static inline void reduce(float* lds, const f32x4 (&acc)[NT][MT], int waves,
+                                       Out&& out) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float* mine = lds + wave * RED_FLOATS_PER_WAVE;
 #pragma unroll
     for (int t = 0; t < NT; ++t)
-      load_tile(tl[t], r.wbase[t], r.sbase[t], r.bbase[t], r.woff[t], r.soff[t], c, K, kg);
-  }
-
-  __device__ static inline void step(const uint16_t* __restrict__ x, const Stage& st, const Rows& r,
-                                     int c, int c_end, int K, char* lds, int buf,
-                                     Tile (&cur)[NT], Tile (&nxt)[NT], f32x4 (&acc)[NT][MT],
-                                     int lane) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) mine[((t * MT + mt) * 4 + j) * 64 + lane] = acc[t][mt][j];
     __syncthreads();
-    const bool more = (c + 1) < c_end;
-    u32x4 xv[SPT];
-    if (more) {
-      stage_load(x, st, c + 1, K, xv);
-      load_tiles(nxt, r, c + 1, K, lane >> 4);
-    }
-    compute_chunk(lds + buf * LDS_BUF, cur, acc, lane);
-    if (more) stage_store(lds + (buf ^ 1) * LDS_BUF, st, xv);
-  }
-
-  // Accumulate chunks [c_begin, c_end) into acc (acc is not cleared here).
-  __device__ static inline void run(const uint16_t* __restrict__ x, const Stage& st, const Rows& r,
-                                    int K, int c_begin, int c_end, char* lds,
-                                    f32x4 (&acc)[NT][MT]) {
-    const int lane = threadIdx.x & 63;
-    Tile ta[NT], tb[NT];
-    {
-      u32x4 xv[SPT];
-      stage_load(x, st, c_begin, K, xv);
-      load_tiles(ta, r, c_begin, K, lane >> 4);
-      stage_store(lds, st, xv);
-    }
-    for (int c = c_begin; c < c_end; c += 2) {
-      step(x, st, r, c, c_end, K, lds, 0, ta, tb, acc, lane);
-      if (c + 1 < c_end) step(x, st, r, c + 1, c_end, K, lds, 1, tb, ta, acc, lane);
+    for (int e = tid; e < RED_FLOATS_PER_WAVE; e += waves * 64) {
+      float s = lds[e];
+      for (int w = 1; w < waves; ++w) s += lds[w * RED_FLOATS_PER_WAVE + e];
+      const int l = e & 63, j = (e >> 6) & 3, tm = e >> 8;
+      out(tm / MT, tm % MT, j, l, s);
     }
   }
 };

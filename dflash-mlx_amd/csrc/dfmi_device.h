@@ -7,10 +7,10 @@
 //
 // Arithmetic scheme.  For one quantisation group g of row n,
 //     sum_k x[m,k] (q[n,k] s + b) = s * sum_k x[m,k] (OFF + q[n,k]) + (b - OFF s) * X[m,g]
-// with X[m,g] = sum_{k in g} x[m,k].  The bracket (OFF + q) is produced with
-// one AND-OR per pair of nibbles: (w & 0x000F000F) | MAGIC is a packed pair of
-// bf16 values 128+q (exponent 2^7, q in the low mantissa bits; f16 uses 1024+q),
-// exact, and feeds v_mfma_f32_16x16x32_{bf16,f16} directly.  The per-group
+// with X[m,g] = sum_{k in g} x[m,k].  The bracket (OFF + q) is produced by bit
+// operations: (w & 0x000F000F) | MAGIC is a packed pair of bf16 values 128+q
+// (exponent 2^7, q in the low mantissa bits; f16 uses 1024+q), exact, and
+// feeds v_mfma_f32_16x16x32_{bf16,f16} directly.  The per-group
 // scale is applied to the fp32 MFMA result, and the bias term is one
 // v_mfma_f32_16x16x4_f32 per four groups (X in the A operand, b - OFF s in the
 // B operand).  Every product is exact and every sum is fp32.
@@ -66,27 +66,47 @@ template <> struct Num<F16> {
   }
 };
 
-// One packed word (8 nibbles q0..q7) -> MFMA operand of 8 16-bit values in the
-// order (q0,q4, q1,q5, q2,q6, q3,q7), each value OFF + q.
+// Dequantisation constants held in registers.  gfx9 VOP3 encodings take no
+// literal operand, so with literal constants the compiler splits
+// (w & mask) | magic into two VOP2 instructions; with the mask in an SGPR and
+// MAGIC in a VGPR (the empty asm statements hide their values) it selects one
+// v_and_or_b32.  Plain C rather than an asm v_and_or_b32 keeps the compiler's
+// hazard tracking (a VALU write to a VGPR an in-flight MFMA still reads).
+struct DqConst {
+  uint32_t mask;   // 0x000F000F
+  uint32_t magic;  // Num<Tag>::MAGIC
+};
+
 template <typename Tag>
-__device__ inline u32x4 dequant_word4(uint32_t w) {
-  constexpr uint32_t M = Num<Tag>::MAGIC;
-  u32x4 r;
-  r.x = (w & 0x000F000Fu) | M;
-  r.y = ((w >> 4) & 0x000F000Fu) | M;
-  r.z = ((w >> 8) & 0x000F000Fu) | M;
-  r.w = ((w >> 12) & 0x000F000Fu) | M;
-  return r;
+__device__ inline DqConst dq_const() {
+  DqConst c;
+  c.mask = 0x000F000Fu;
+  c.magic = Num<Tag>::MAGIC;
+  asm volatile("" : "+s"(c.mask));
+  asm volatile("" : "+v"(c.magic));
+  return c;
 }
 
-// 8 consecutive activations (x0..x7 as four packed pairs) -> the same element
-// order as dequant_word4: (x0,x4, x1,x5, x2,x6, x3,x7).
-__device__ inline u32x4 permute_x8(u32x4 v) {
+// One packed word (8 nibbles q0..q7, k order) -> MFMA operand of 8 16-bit
+// values OFF + q0 .. OFF + q7 in k order, so the activations feed the MFMA
+// unpermuted.  Nine VALU operations (dq = dq_const<Tag>()):
+//   lo = (w & 0x000F000F) | MAGIC          -> 16-bit pairs (q0, q4)
+//   mi = ((w >> 8) & 0x000F000F) | MAGIC   -> (q2, q6)
+//   od = (w >> 4) & 0x0F0F0F0F             -> bytes q1, q3, q5, q7
+// and four byte permutes that put an odd nibble byte next to an even one,
+// each 16-bit value keeping the MAGIC high byte.
+template <typename Tag>
+__device__ inline u32x4 dequant_word4(uint32_t w, const DqConst& dq) {
+  const uint32_t lo = (w & dq.mask) | dq.magic;
+  const uint32_t mi = ((w >> 8) & dq.mask) | dq.magic;
+  const uint32_t od = (w >> 4) & 0x0F0F0F0Fu;
   u32x4 r;
-  r.x = __builtin_amdgcn_perm(v.z, v.x, 0x05040100u);
-  r.y = __builtin_amdgcn_perm(v.z, v.x, 0x07060302u);
-  r.z = __builtin_amdgcn_perm(v.w, v.y, 0x05040100u);
-  r.w = __builtin_amdgcn_perm(v.w, v.y, 0x07060302u);
+  // __builtin_amdgcn_perm(S0, S1, sel): selector byte 0..3 picks a byte of
+  // S1, 4..7 a byte of S0.
+  r.x = __builtin_amdgcn_perm(od, lo, 0x03040100u);  // (q0, q1)
+  r.y = __builtin_amdgcn_perm(od, mi, 0x03050100u);  // (q2, q3)
+  r.z = __builtin_amdgcn_perm(od, lo, 0x03060302u);  // (q4, q5)
+  r.w = __builtin_amdgcn_perm(od, mi, 0x03070302u);  // (q6, q7)
   return r;
 }
 

@@ -2,18 +2,23 @@
 // length against the drafted block, bonus token.
 //
 //  * lmhead_greedy_kernel: the lm_head matmul (same main loop as the dense
-//    qmm, full K per workgroup, 128 vocabulary rows per workgroup) whose
-//    epilogue rounds each logit to the activation dtype (the dtype the
+//    qmm: 16*NT vocabulary rows per workgroup, K split over its wavefronts)
+//    whose epilogue rounds each logit to the activation dtype (the dtype the
 //    reference's logits carry), applies the optional Gemma softcap and the
 //    suppress mask, and reduces to a per-row (value, index) argmax key.  The
 //    logits never reach HBM unless the caller asks for them.
 //  * greedy_kernel: the same reduction over logits already in memory.
 //
 // Cross-workgroup reduction: a 64-bit key (monotone value bits << 32 |
-// ~index) per row, combined with atomicMax -- max is order-independent, so
-// the winner (largest value, then lowest index) is deterministic.  The last
-// workgroup to finish (atomic counter) turns the keys into tokens, computes
-// accept / bonus and clears the keys and the counter for the next call.
+// ~index) per row, combined with a device-scope atomic max -- max is
+// order-independent, so the winner (largest value, then lowest index) is
+// deterministic.  All cross-workgroup communication is atomic
+// read-modify-writes on the workspace: every workgroup waits for its key
+// RMWs to return before its counter RMW, and the workgroup whose counter RMW
+// returns total-1 (the last) reads each key with an exchange that also
+// clears it, computes accept / bonus and clears the counter.  No plain
+// store is published across workgroups, so no cache writeback or invalidate
+// (the cost of a device-scope fence on this GPU) is needed.
 #include <math.h>
 
 #include "dfmi_core.h"
@@ -22,6 +27,7 @@
 namespace dfmi {
 
 constexpr int kMaxGreedyRows = 32;
+constexpr int kGreedyThreads = 256;
 
 struct GreedyOut {
   unsigned long long* keys;  // [M] workspace, zero between calls
@@ -33,28 +39,38 @@ struct GreedyOut {
   int M;
 };
 
-// Called by every workgroup after it has published its keys.  The last one
-// to arrive finalises.
-__device__ inline void greedy_finish(const GreedyOut& o, unsigned total_blocks) {
+__device__ inline unsigned long long umax64(unsigned long long a, unsigned long long b) {
+  return a > b ? a : b;
+}
+
+// Publish this workgroup's keys for rows [r0, r1) (s_best[m] in LDS) and, in
+// the last workgroup to arrive, turn the keys into tokens, accept and bonus.
+__device__ inline void greedy_publish_and_finish(const GreedyOut& o,
+                                                 const unsigned long long* s_best, int r0,
+                                                 int r1, unsigned total_blocks) {
   __shared__ int s_last;
-  __threadfence();
+  __shared__ uint32_t s_post[kMaxGreedyRows];
+  __shared__ int s_sink;
+  const int tid = threadIdx.x;
+  if (tid >= r0 && tid < r1) {
+    const unsigned long long old = __hip_atomic_fetch_max(
+        &o.keys[tid], s_best[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (old == ~0ull) s_sink = 1;  // consume the result: the RMW has completed
+  }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    const unsigned prev = atomicAdd(o.counter, 1u);
+  if (tid == 0) {
+    const unsigned prev =
+        __hip_atomic_fetch_add(o.counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_last = (prev == total_blocks - 1) ? 1 : 0;
   }
   __syncthreads();
   if (!s_last) return;
-  __threadfence();
-  __shared__ uint32_t s_post[kMaxGreedyRows];
-  const int tid = threadIdx.x;
   if (tid < o.M) {
     const unsigned long long k =
-        __hip_atomic_load(&o.keys[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_exchange(&o.keys[tid], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const uint32_t tok = key_index(k);
     s_post[tid] = tok;
     o.posterior[tid] = tok;
-    __hip_atomic_store(&o.keys[tid], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
   if (tid == 0) {
@@ -64,25 +80,8 @@ __device__ inline void greedy_finish(const GreedyOut& o, unsigned total_blocks) 
       if (o.accept_len) o.accept_len[0] = a;
       if (o.bonus) o.bonus[0] = s_post[a];
     }
-    __hip_atomic_store(o.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_exchange(o.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-}
-
-__device__ inline unsigned long long umax64(unsigned long long a, unsigned long long b) {
-  return a > b ? a : b;
-}
-
-// Max of a 64-bit key over the 16 lanes of each row of 16 (lanes l, l^1 .. l^8).
-__device__ inline unsigned long long max16(unsigned long long v) {
-#pragma unroll
-  for (int d = 1; d < 16; d <<= 1) v = umax64(v, __shfl_xor(v, d, 64));
-  return v;
-}
-
-__device__ inline unsigned long long max64(unsigned long long v) {
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) v = umax64(v, __shfl_xor(v, d, 64));
-  return v;
 }
 
 template <typename Tag>
@@ -117,34 +116,29 @@ struct LmArgs {
   GreedyOut out;
 };
 
-template <typename Tag, int GS, int MT, bool KFULL>
-__global__ __launch_bounds__(kThreads) void lmhead_greedy_kernel(LmArgs a) {
-  constexpr int NT = 2;
-  using C = Core<Tag, GS, MT, NT, KFULL>;
-  constexpr int NB = kWaves * 16 * NT;
-  __shared__ __attribute__((aligned(16))) char lds[C::LDS_BYTES];
-  __shared__ unsigned long long s_keys[kWaves][16 * MT];
+constexpr int kLmTiles = 4;  // 64 vocabulary rows per workgroup
 
-  const int nb = blockIdx.x;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+template <typename Tag, int GS, int MT, bool KFULL>
+__global__ __launch_bounds__(kMaxWaves * 64) void lmhead_greedy_kernel(LmArgs a) {
+  constexpr int NT = kLmTiles;
+  using C = Core<Tag, GS, MT, NT, KFULL>;
+  __shared__ __attribute__((aligned(16))) float lds[C::LDS_BYTES / 4];
+  __shared__ unsigned long long s_best[16 * MT];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  // wave-uniform values in scalar registers, so the chunk loop is a scalar loop
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int waves = blockDim.x >> 6;
+  const int n0 = blockIdx.x * 16 * NT;
+  if (tid < 16 * MT) s_best[tid] = 0ull;
+
+  const typename C::XRows xr = C::x_rows(0, a.M, a.K, lane);
   const uint32_t kw = (uint32_t)(a.K / 8);
   const uint32_t kgrp = (uint32_t)(a.K / GS);
-
-  typename C::Stage st;
-#pragma unroll
-  for (int i = 0; i < C::SPT; ++i) {
-    const int slot = tid + kThreads * i;
-    int m, kk;
-    C::slot_geometry(slot, m, kk);
-    st.xoff[i] = m < a.M ? (int64_t)m * a.K : -1;
-    st.kk[i] = kk;
-    st.lds[i] = slot * 16;
-  }
-  const int col0 = nb * NB + wave * 16 * NT;
   typename C::Rows r;
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
-    const int row = min(col0 + t * 16 + (lane & 15), a.V - 1);
+    const int row = min(n0 + t * 16 + (lane & 15), a.V - 1);
     r.wbase[t] = a.w;
     r.sbase[t] = a.s;
     r.bbase[t] = a.b;
@@ -156,39 +150,25 @@ __global__ __launch_bounds__(kThreads) void lmhead_greedy_kernel(LmArgs a) {
   for (int t = 0; t < NT; ++t)
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[t][mt] = zero4();
-  C::run(a.h, st, r, a.K, 0, a.chunks, lds, acc);
+  const int kr = (wave + (int)blockIdx.x) % waves;
+  const int c0 = kr * a.chunks / waves;
+  const int c1 = (kr + 1) * a.chunks / waves;
+  if (c1 > c0) C::run(a.h, xr, r, a.K, c0, c1, acc);
 
-  const int kg = lane >> 4, col = lane & 15;
   const float capr = a.softcap > 0.f ? round_t<Tag>(a.softcap) : 0.f;
   const float neg = round_t<Tag>(-1e9f);
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int m = mt * 16 + 4 * kg + j;
-      unsigned long long best = 0ull;
-#pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        const int n = col0 + t * 16 + col;
-        if (m < a.M && n < a.V) {
-          float v = logit_value<Tag>(acc[t][mt][j], capr);
-          if (a.logits) a.logits[(int64_t)m * a.V + n] = Num<Tag>::f2h(v);
-          if (a.mask && a.mask[n]) v = neg;
-          best = umax64(best, argmax_key(v, (uint32_t)n));
-        }
-      }
-      best = max16(best);
-      if (col == 0) s_keys[wave][mt * 16 + 4 * kg + j] = best;
+  C::reduce(lds, acc, waves, [&](int t, int mt, int j, int l, float sum) {
+    const int m = mt * 16 + 4 * (l >> 4) + j;
+    const int n = n0 + t * 16 + (l & 15);
+    if (m < a.M && n < a.V) {
+      float v = logit_value<Tag>(sum, capr);
+      if (a.logits) a.logits[(int64_t)m * a.V + n] = Num<Tag>::f2h(v);
+      if (a.mask && a.mask[n]) v = neg;
+      atomicMax(&s_best[m], argmax_key(v, (uint32_t)n));
     }
-  }
+  });
   __syncthreads();
-  if (tid < a.M) {
-    unsigned long long best = s_keys[0][tid];
-#pragma unroll
-    for (int w = 1; w < kWaves; ++w) best = umax64(best, s_keys[w][tid]);
-    atomicMax(&a.out.keys[tid], best);
-  }
-  greedy_finish(a.out, (unsigned)a.n_blocks);
+  greedy_publish_and_finish(a.out, s_best, 0, a.M, (unsigned)a.n_blocks);
 }
 
 struct GreedyArgs {
@@ -202,19 +182,21 @@ struct GreedyArgs {
 
 constexpr int kGreedyPerBlock = 4096;
 
-__global__ __launch_bounds__(kThreads) void greedy_kernel(GreedyArgs a) {
-  __shared__ unsigned long long s_keys[kWaves];
+__global__ __launch_bounds__(kGreedyThreads) void greedy_kernel(GreedyArgs a) {
+  __shared__ unsigned long long s_best[kMaxGreedyRows];
   const int m = blockIdx.y;
   const int v0 = blockIdx.x * a.per_block;
   const int v1 = min(a.V, v0 + a.per_block);
   const int tid = threadIdx.x;
+  if (tid < kMaxGreedyRows) s_best[tid] = 0ull;
+  __syncthreads();
   float neg;
   if (a.dtype == DFMI_BF16) neg = Num<BF16>::h2f(Num<BF16>::f2h(-1e9f));
   else if (a.dtype == DFMI_F16) neg = Num<F16>::h2f(Num<F16>::f2h(-1e9f));
   else neg = -1e9f;
   unsigned long long best = 0ull;
   const int64_t row = (int64_t)m * a.V;
-  for (int v = v0 + tid; v < v1; v += kThreads) {
+  for (int v = v0 + tid; v < v1; v += kGreedyThreads) {
     float x;
     if (a.dtype == DFMI_BF16) x = Num<BF16>::h2f(static_cast<const uint16_t*>(a.logits)[row + v]);
     else if (a.dtype == DFMI_F16) x = Num<F16>::h2f(static_cast<const uint16_t*>(a.logits)[row + v]);
@@ -222,16 +204,11 @@ __global__ __launch_bounds__(kThreads) void greedy_kernel(GreedyArgs a) {
     if (a.mask && a.mask[v]) x = neg;
     best = umax64(best, argmax_key(x, (uint32_t)v));
   }
-  best = max64(best);
-  if ((tid & 63) == 0) s_keys[tid >> 6] = best;
-  __syncthreads();
-  if (tid == 0) {
-    unsigned long long b = s_keys[0];
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w) b = umax64(b, s_keys[w]);
-    atomicMax(&a.out.keys[m], b);
-  }
-  greedy_finish(a.out, gridDim.x * gridDim.y);
+  for (int d = 1; d < 64; d <<= 1) best = umax64(best, __shfl_xor(best, d, 64));
+  if ((tid & 63) == 0) atomicMax(&s_best[m], best);
+  __syncthreads();
+  greedy_publish_and_finish(a.out, s_best, m, m + 1, gridDim.x * gridDim.y);
 }
 
 __global__ void accept_kernel(const uint32_t* drafted, const uint32_t* posterior, int64_t L,
@@ -263,27 +240,27 @@ static int bind_out(GreedyOut& o, void* ws, size_t ws_bytes, int64_t M, uint32_t
 }
 
 template <typename Tag, int GS, int MT>
-static void launch_lm(bool kfull, int blocks, hipStream_t st, const LmArgs& a) {
+static void launch_lm(bool kfull, int blocks, int waves, hipStream_t st, const LmArgs& a) {
   if (kfull)
-    hipLaunchKernelGGL((lmhead_greedy_kernel<Tag, GS, MT, true>), dim3(blocks), dim3(kThreads), 0,
-                       st, a);
+    hipLaunchKernelGGL((lmhead_greedy_kernel<Tag, GS, MT, true>), dim3(blocks), dim3(64 * waves),
+                       0, st, a);
   else
-    hipLaunchKernelGGL((lmhead_greedy_kernel<Tag, GS, MT, false>), dim3(blocks), dim3(kThreads),
+    hipLaunchKernelGGL((lmhead_greedy_kernel<Tag, GS, MT, false>), dim3(blocks), dim3(64 * waves),
                        0, st, a);
 }
 
 template <typename Tag>
-static void launch_lm_tag(int gs, int mt, bool kfull, int blocks, hipStream_t st,
+static void launch_lm_tag(int gs, int mt, bool kfull, int blocks, int waves, hipStream_t st,
                           const LmArgs& a) {
   if (gs == 32) {
-    if (mt == 1) launch_lm<Tag, 32, 1>(kfull, blocks, st, a);
-    else launch_lm<Tag, 32, 2>(kfull, blocks, st, a);
+    if (mt == 1) launch_lm<Tag, 32, 1>(kfull, blocks, waves, st, a);
+    else launch_lm<Tag, 32, 2>(kfull, blocks, waves, st, a);
   } else if (gs == 64) {
-    if (mt == 1) launch_lm<Tag, 64, 1>(kfull, blocks, st, a);
-    else launch_lm<Tag, 64, 2>(kfull, blocks, st, a);
+    if (mt == 1) launch_lm<Tag, 64, 1>(kfull, blocks, waves, st, a);
+    else launch_lm<Tag, 64, 2>(kfull, blocks, waves, st, a);
   } else {
-    if (mt == 1) launch_lm<Tag, 128, 1>(kfull, blocks, st, a);
-    else launch_lm<Tag, 128, 2>(kfull, blocks, st, a);
+    if (mt == 1) launch_lm<Tag, 128, 1>(kfull, blocks, waves, st, a);
+    else launch_lm<Tag, 128, 2>(kfull, blocks, waves, st, a);
   }
 }
 
@@ -321,7 +298,8 @@ extern "C" int dfmi_greedy_accept(const void* logits, int logits_dtype, const ui
   a.V = (int)V;
   a.per_block = kGreedyPerBlock;
   const dim3 grid((unsigned)((V + kGreedyPerBlock - 1) / kGreedyPerBlock), (unsigned)M);
-  hipLaunchKernelGGL(greedy_kernel, grid, dim3(kThreads), 0, static_cast<hipStream_t>(stream), a);
+  hipLaunchKernelGGL(greedy_kernel, grid, dim3(kGreedyThreads), 0, static_cast<hipStream_t>(stream),
+                     a);
   return check_launch("dfmi_greedy_accept");
 }
 
@@ -368,13 +346,14 @@ extern "C" int dfmi_lmhead_greedy_accept(const void* h, int h_dtype, const uint3
   a.K = (int)K;
   a.V = (int)V;
   a.chunks = (int)((K + kChunkK - 1) / kChunkK);
-  const int nb_cols = kWaves * 16 * 2;
+  const int nb_cols = 16 * kLmTiles;
   a.n_blocks = (int)((V + nb_cols - 1) / nb_cols);
   const bool kfull = (K % kChunkK) == 0;
   const int mt = M <= 16 ? 1 : 2;
+  const int waves = a.chunks < kMaxWaves ? a.chunks : kMaxWaves;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (h_dtype == DFMI_BF16) launch_lm_tag<BF16>(group_size, mt, kfull, a.n_blocks, st, a);
-  else launch_lm_tag<F16>(group_size, mt, kfull, a.n_blocks, st, a);
+  if (h_dtype == DFMI_BF16) launch_lm_tag<BF16>(group_size, mt, kfull, a.n_blocks, waves, st, a);
+  else launch_lm_tag<F16>(group_size, mt, kfull, a.n_blocks, waves, st, a);
   return check_launch("dfmi_lmhead_greedy_accept");
 }
 

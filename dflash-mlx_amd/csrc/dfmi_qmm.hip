@@ -1,18 +1,18 @@
 // Dense affine int4 qmm: y[M,N] = x[M,K] . dequant(W)^T on gfx950.
 //
-// Grid: one workgroup (4 wavefronts) per (output block of 64*NT columns,
-// K split).  Each wavefront owns NT 16-column tiles of the block and all M
-// rows (MT 16-row MFMA blocks, M <= 32; larger M tiles over grid.y).  When a
-// block is split along K over `kpg` workgroups, each writes an fp32 partial
-// and the last one to finish (atomic counter) sums the partials in split
-// order -- the result does not depend on arrival order -- and writes y.  The
-// splits of one block are mapped to one XCD (workgroup ids are dealt to the 8
-// XCDs round-robin) so the partials stay in that XCD's L2.
+// Grid: one workgroup per 16*NT output columns (and per 32-row block of M
+// when M > 32).  The workgroup's W wavefronts split K between them and sum
+// their partial tiles through LDS (Core::reduce), so every output element is
+// written once, by one workgroup, with no atomics and no device-scope fence.
+// NT grows with N (1, 2, 4 tiles per wavefront) so that every workgroup
+// streams enough weight bytes to amortise its activation reads (x is read
+// from L2 by every workgroup: x bytes / weight bytes = 57 / (16*NT)).
 #include <algorithm>
 #include <cmath>
 
 #include "dfmi_core.h"
 #include "dfmi_host.h"
+#include "dfmi_stream.h"
 
 namespace dfmi {
 
@@ -22,59 +22,29 @@ struct DenseArgs {
   const uint16_t* s;
   const uint16_t* b;
   uint16_t* y;
-  float* partials;
-  uint32_t* counters;
   int M, K, N;
-  int kpg;       // workgroups sharing one output block along K
-  int chunks;    // ceil(K / 256)
-  int n_blocks;  // ceil(N / (64 * NT))
-  int xcd_map;   // 1: the K splits of a block are dealt to the same XCD
+  int chunks;  // ceil(K / 256)
 };
 
 template <typename Tag, int GS, int MT, int NT, bool KFULL>
-__global__ __launch_bounds__(kThreads) void qmm_dense_kernel(DenseArgs a) {
+__global__ __launch_bounds__(kMaxWaves * 64) void qmm_dense_kernel(DenseArgs a) {
   using C = Core<Tag, GS, MT, NT, KFULL>;
-  constexpr int NB = kWaves * 16 * NT;
-  __shared__ __attribute__((aligned(16))) char lds[C::LDS_BYTES];
-  __shared__ int s_last;
+  __shared__ __attribute__((aligned(16))) float lds[C::LDS_BYTES / 4];
 
-  int nb, kp;
-  {
-    const int L = blockIdx.x;
-    if (a.xcd_map) {
-      const int xcd = L & 7, j = L >> 3;
-      const int nbl = j / a.kpg;
-      kp = j - nbl * a.kpg;
-      nb = nbl * 8 + xcd;
-    } else {
-      nb = L / a.kpg;
-      kp = L - nb * a.kpg;
-    }
-  }
-  if (nb >= a.n_blocks) return;  // uniform for the block, before any barrier
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  // wave-uniform values in scalar registers, so the chunk loop is a scalar loop
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int waves = blockDim.x >> 6;
+  const int n0 = blockIdx.x * 16 * NT;
   const int m_base = blockIdx.y * 16 * MT;
+
+  const typename C::XRows xr = C::x_rows(m_base, a.M, a.K, lane);
   const uint32_t kw = (uint32_t)(a.K / 8);
   const uint32_t kgrp = (uint32_t)(a.K / GS);
-
-  typename C::Stage st;
-#pragma unroll
-  for (int i = 0; i < C::SPT; ++i) {
-    const int slot = tid + kThreads * i;
-    int m, kk;
-    C::slot_geometry(slot, m, kk);
-    const int mm = m_base + m;
-    st.xoff[i] = mm < a.M ? (int64_t)mm * a.K : -1;
-    st.kk[i] = kk;
-    st.lds[i] = slot * 16;
-  }
-
-  const int col0 = nb * NB + wave * 16 * NT;
   typename C::Rows r;
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
-    const int row = min(col0 + t * 16 + (lane & 15), a.N - 1);
+    const int row = min(n0 + t * 16 + (lane & 15), a.N - 1);
     r.wbase[t] = a.w;
     r.sbase[t] = a.s;
     r.bbase[t] = a.b;
@@ -82,76 +52,28 @@ __global__ __launch_bounds__(kThreads) void qmm_dense_kernel(DenseArgs a) {
     r.soff[t] = (uint32_t)row * kgrp;
   }
 
-  const int c_begin = (int)((int64_t)kp * a.chunks / a.kpg);
-  const int c_end = (int)((int64_t)(kp + 1) * a.chunks / a.kpg);
   f32x4 acc[NT][MT];
 #pragma unroll
   for (int t = 0; t < NT; ++t)
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[t][mt] = zero4();
+  // Rotate the K-range of each wavefront by workgroup, so that concurrently
+  // running workgroups do not all read the same activation lines at once.
+  const int kr = (wave + (int)blockIdx.x) % waves;
+  const int c0 = kr * a.chunks / waves;
+  const int c1 = (kr + 1) * a.chunks / waves;
+  if (c1 > c0) C::run(a.x, xr, r, a.K, c0, c1, acc);
 
-  C::run(a.x, st, r, a.K, c_begin, c_end, lds, acc);
-
-  const int kg = lane >> 4, col = lane & 15;
-  if (a.kpg == 1) {
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const int n = col0 + t * 16 + col;
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int m = m_base + mt * 16 + 4 * kg + j;
-          if (m < a.M && n < a.N) a.y[(int64_t)m * a.N + n] = Num<Tag>::f2h(acc[t][mt][j]);
-        }
-    }
-    return;
-  }
-
-  // K split: publish this split's partial, the last arriver reduces.
-  float* part = a.partials + (int64_t)kp * a.M * a.N;
-#pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    const int n = col0 + t * 16 + col;
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int m = mt * 16 + 4 * kg + j;  // M <= 32 on this path (grid.y == 1)
-        if (m < a.M && n < a.N) part[(int64_t)m * a.N + n] = acc[t][mt][j];
-      }
-  }
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    const unsigned prev = atomicAdd(&a.counters[nb], 1u);
-    s_last = (prev == (unsigned)(a.kpg - 1)) ? 1 : 0;
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  const int n0 = nb * NB;
-  for (int idx = tid; idx < a.M * NB; idx += kThreads) {
-    const int m = idx / NB, n = n0 + idx % NB;
-    if (n < a.N) {
-      float sum = 0.f;
-      for (int q = 0; q < a.kpg; ++q) sum += a.partials[((int64_t)q * a.M + m) * a.N + n];
-      a.y[(int64_t)m * a.N + n] = Num<Tag>::f2h(sum);
-    }
-  }
-  if (tid == 0) a.counters[nb] = 0u;
+  C::reduce(lds, acc, waves, [&](int t, int mt, int j, int l, float v) {
+    const int m = m_base + mt * 16 + 4 * (l >> 4) + j;
+    const int n = n0 + t * 16 + (l & 15);
+    if (m < a.M && n < a.N) a.y[(int64_t)m * a.N + n] = Num<Tag>::f2h(v);
+  });
 }
 
-// Counters live in a fixed-size region at the start of every qmm workspace,
-// so calls of different shapes agree on where they are (a counter is only
-// ever zero between calls).
-constexpr size_t kCounterBytes = 65536;
-constexpr int kMaxCounters = (int)(kCounterBytes / 4);
-
 struct DensePlan {
-  int MT, NT, kpg, chunks, n_blocks, grid_x, grid_y, xcd_map;
+  int MT, NT, waves, chunks, grid_x, grid_y;
   bool kfull;
-  size_t counters_bytes, ws_bytes;
 };
 
 static int plan_dense(int64_t M, int64_t K, int64_t N, const dfmi_qmm_tuning* tune, DensePlan& p) {
@@ -159,55 +81,43 @@ static int plan_dense(int64_t M, int64_t K, int64_t N, const dfmi_qmm_tuning* tu
   p.grid_y = M <= 32 ? 1 : (int)((M + 31) / 32);
   p.chunks = (int)((K + kChunkK - 1) / kChunkK);
   p.kfull = (K % kChunkK) == 0;
-  int nt = (tune && tune->tiles_per_wave) ? tune->tiles_per_wave : (((N + 127) / 128) >= 64 ? 2 : 1);
-  if (nt != 1 && nt != 2) {
-    set_error("dfmi_qmm: tiles_per_wave must be 1 or 2 (got %d)", nt);
+  int nt = (tune && tune->tiles_per_wave) ? tune->tiles_per_wave
+                                          : (N <= 8192 ? 1 : (N <= 32768 ? 2 : 4));
+  if (nt != 1 && nt != 2 && nt != 4) {
+    set_error("dfmi_qmm: tiles_per_wave must be 1, 2 or 4 (got %d)", nt);
+    return DFMI_EINVAL;
+  }
+  int waves = (tune && tune->waves_per_block) ? tune->waves_per_block : kMaxWaves;
+  if (waves < 1 || waves > kMaxWaves) {
+    set_error("dfmi_qmm: waves_per_block must be 1..%d (got %d)", kMaxWaves, waves);
     return DFMI_EINVAL;
   }
   p.NT = nt;
-  const int64_t nb_cols = (int64_t)kWaves * 16 * nt;
-  p.n_blocks = (int)((N + nb_cols - 1) / nb_cols);
-  int kpg;
-  if (M > 32) {
-    kpg = 1;
-  } else if (tune && tune->k_splits > 0) {
-    kpg = tune->k_splits;
-  } else {
-    kpg = (int)std::lround(512.0 / (double)p.n_blocks);
-    kpg = std::min(kpg, std::max(1, p.chunks / 2));
-  }
-  p.kpg = std::max(1, std::min(kpg, p.chunks));
-  if (p.n_blocks > kMaxCounters) p.kpg = 1;
-  p.xcd_map = (p.n_blocks % 8 == 0) ? 1 : 0;
-  p.grid_x = p.n_blocks * p.kpg;
-  if (p.kpg > 1) {
-    p.counters_bytes = kCounterBytes;
-    p.ws_bytes = p.counters_bytes + (size_t)p.kpg * (size_t)M * (size_t)N * 4u;
-  } else {
-    p.counters_bytes = 0;
-    p.ws_bytes = 0;
-  }
+  p.waves = std::min(waves, p.chunks);
+  p.grid_x = (int)((N + 16 * nt - 1) / (16 * nt));
   return DFMI_OK;
 }
 
 template <typename Tag, int GS, int MT, int NT>
-static void launch_kf(bool kfull, dim3 g, hipStream_t st, const DenseArgs& a) {
-  if (kfull)
-    hipLaunchKernelGGL((qmm_dense_kernel<Tag, GS, MT, NT, true>), g, dim3(kThreads), 0, st, a);
+static void launch_kf(const DensePlan& p, hipStream_t st, const DenseArgs& a) {
+  const dim3 g(p.grid_x, p.grid_y), blk(64 * p.waves);
+  if (p.kfull)
+    hipLaunchKernelGGL((qmm_dense_kernel<Tag, GS, MT, NT, true>), g, blk, 0, st, a);
   else
-    hipLaunchKernelGGL((qmm_dense_kernel<Tag, GS, MT, NT, false>), g, dim3(kThreads), 0, st, a);
+    hipLaunchKernelGGL((qmm_dense_kernel<Tag, GS, MT, NT, false>), g, blk, 0, st, a);
+}
+
+template <typename Tag, int GS, int MT>
+static void launch_mt(const DensePlan& p, hipStream_t st, const DenseArgs& a) {
+  if (p.NT == 1) launch_kf<Tag, GS, MT, 1>(p, st, a);
+  else if (p.NT == 2) launch_kf<Tag, GS, MT, 2>(p, st, a);
+  else launch_kf<Tag, GS, MT, 4>(p, st, a);
 }
 
 template <typename Tag, int GS>
 static void launch_gs(const DensePlan& p, hipStream_t st, const DenseArgs& a) {
-  const dim3 g(p.grid_x, p.grid_y);
-  if (p.MT == 1) {
-    if (p.NT == 1) launch_kf<Tag, GS, 1, 1>(p.kfull, g, st, a);
-    else launch_kf<Tag, GS, 1, 2>(p.kfull, g, st, a);
-  } else {
-    if (p.NT == 1) launch_kf<Tag, GS, 2, 1>(p.kfull, g, st, a);
-    else launch_kf<Tag, GS, 2, 2>(p.kfull, g, st, a);
-  }
+  if (p.MT == 1) launch_mt<Tag, GS, 1>(p, st, a);
+  else launch_mt<Tag, GS, 2>(p, st, a);
 }
 
 template <typename Tag>
@@ -215,6 +125,215 @@ static void launch_tag(int gs, const DensePlan& p, hipStream_t st, const DenseAr
   if (gs == 32) launch_gs<Tag, 32>(p, st, a);
   else if (gs == 64) launch_gs<Tag, 64>(p, st, a);
   else launch_gs<Tag, 128>(p, st, a);
+}
+
+// ---------------------------------------------------------------------------
+// Fast path (Stream main loop): M <= 32, K % 256 == 0, K % (8 * group) == 0.
+// A workgroup of 4 wavefronts owns 64 weight rows and a range of the K
+// chunks; its wavefronts' partial tiles are summed through LDS.  When the K
+// range is split over kp workgroups, each writes its fp32 partial with
+// device-coherent stores (agent-scope relaxed atomic stores: write-through,
+// no cache flush), waits for them to complete, then bumps the block's counter
+// with an atomic RMW; the workgroup that takes the counter to kp sums the kp
+// partials in split order (device-coherent loads) and writes y, so the result
+// does not depend on arrival order.  No device-scope fence is needed because
+// no plain store is published across workgroups.
+
+constexpr size_t kCounterBytes = 65536;
+constexpr int kMaxCounters = (int)(kCounterBytes / 4);
+
+struct StreamArgs {
+  const uint16_t* x;
+  const uint32_t* w;
+  const uint16_t* s;
+  const uint16_t* b;
+  uint16_t* y;
+  float* partials;     // [kp][M][N] fp32 (kp > 1)
+  uint32_t* counters;  // [n_blocks] (kp > 1), zero between calls
+  int M, K, N;
+  int chunks;
+  int kp;
+  int n_blocks;
+  int xcd_map;
+};
+
+template <typename Tag, int GS, int MT>
+__global__ __launch_bounds__(kStreamThreads) void qmm_stream_kernel(StreamArgs a) {
+  using S = Stream<Tag, GS, MT>;
+  int nb, kpi;
+  {
+    const int L = blockIdx.x;
+    if (a.xcd_map) {
+      // consecutive workgroup ids go to different XCDs (id & 7): give the
+      // kp splits of one block to one XCD so the block's partials and
+      // counter stay in one L2
+      const int xcd = L & 7, j = L >> 3;
+      const int nbl = j / a.kp;
+      kpi = j - nbl * a.kp;
+      nb = nbl * 8 + xcd;
+    } else {
+      nb = L / a.kp;
+      kpi = L - nb * a.kp;
+    }
+  }
+  if (nb >= a.n_blocks) return;  // uniform, before any barrier
+  typename S::Ctx cx;
+  cx.x = a.x;
+  cx.w = a.w;
+  cx.s = a.s;
+  cx.b = a.b;
+  cx.K = a.K;
+  cx.M = a.M;
+  cx.N = a.N;
+  cx.groups = a.K / GS;
+  cx.n0 = nb * S::NB;
+  cx.lane = threadIdx.x & 63;
+  cx.wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c0 = (int)((int64_t)kpi * a.chunks / a.kp);
+  const int c1 = (int)((int64_t)(kpi + 1) * a.chunks / a.kp);
+  f32x4 acc[S::NT][MT];
+#pragma unroll
+  for (int t = 0; t < S::NT; ++t)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[t][mt] = zero4();
+  S::run(cx, c0, c1, acc);
+
+  // sum the 4 wavefronts' partial tiles through LDS (the stages are free:
+  // every DMA has landed and every wavefront is past its last LDS read)
+  __syncthreads();
+  float* red = reinterpret_cast<float*>(dfmi_smem);
+  {
+    float* mine = red + cx.wave * S::RED_FLOATS;
+#pragma unroll
+    for (int t = 0; t < S::NT; ++t)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) mine[((t * MT + mt) * 4 + j) * 64 + cx.lane] = acc[t][mt][j];
+  }
+  __syncthreads();
+  constexpr int PER = S::RED_FLOATS / kStreamThreads;
+  float v[PER];
+  int mi[PER], ni[PER];
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    const int e = q * kStreamThreads + threadIdx.x;
+    v[q] = red[e] + red[S::RED_FLOATS + e] + red[2 * S::RED_FLOATS + e] + red[3 * S::RED_FLOATS + e];
+    const int l = e & 63, j = (e >> 6) & 3, tm = e >> 8;
+    ni[q] = cx.n0 + (tm / MT) * 16 + (l & 15);
+    mi[q] = (tm % MT) * 16 + 4 * (l >> 4) + j;
+  }
+  if (a.kp == 1) {
+#pragma unroll
+    for (int q = 0; q < PER; ++q)
+      if (mi[q] < a.M && ni[q] < a.N) a.y[(int64_t)mi[q] * a.N + ni[q]] = Num<Tag>::f2h(v[q]);
+    return;
+  }
+  float* part = a.partials + (int64_t)kpi * a.M * a.N;
+#pragma unroll
+  for (int q = 0; q < PER; ++q)
+    if (mi[q] < a.M && ni[q] < a.N)
+      __hip_atomic_store(part + (int64_t)mi[q] * a.N + ni[q], v[q], __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+  int* s_last = reinterpret_cast<int*>(dfmi_smem);  // red[0], already consumed
+  stage_barrier<0>();  // every partial store of the workgroup has completed
+  if (threadIdx.x == 0) {
+    const unsigned prev =
+        __hip_atomic_fetch_add(&a.counters[nb], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *s_last = (prev == (unsigned)(a.kp - 1)) ? 1 : 0;
+  }
+  stage_barrier<0>();
+  if (!*s_last) return;
+  for (int idx = threadIdx.x; idx < a.M * S::NB; idx += kStreamThreads) {
+    const int m = idx / S::NB, n = cx.n0 + idx % S::NB;
+    if (n < a.N) {
+      float sum = 0.f;
+      for (int q = 0; q < a.kp; ++q)
+        sum += __hip_atomic_load(a.partials + ((int64_t)q * a.M + m) * a.N + n, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+      a.y[(int64_t)m * a.N + n] = Num<Tag>::f2h(sum);
+    }
+  }
+  if (threadIdx.x == 0)
+    __hip_atomic_exchange(&a.counters[nb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+struct StreamPlan {
+  int MT, kp, chunks, n_blocks, grid_x, xcd_map, lds;
+  size_t ws_bytes;
+};
+
+static bool stream_eligible(int64_t M, int64_t K, int gs) {
+  return M <= 32 && K % kChunkK == 0 && K % (8 * gs) == 0;
+}
+
+static int plan_stream(int64_t M, int64_t K, int64_t N, int gs, const dfmi_qmm_tuning* tune,
+                       StreamPlan& p) {
+  (void)gs;
+  p.MT = M <= 16 ? 1 : 2;
+  p.chunks = (int)(K / kChunkK);
+  p.n_blocks = (int)((N + kStreamRows - 1) / kStreamRows);
+  int kp;
+  if (tune && tune->k_splits > 0) {
+    kp = tune->k_splits;
+  } else {
+    // one workgroup per CU on 256 CUs, at least 4 chunks per split (every
+    // split pays a pipeline fill and the partial-sum epilogue)
+    kp = (int)std::lround(256.0 / (double)p.n_blocks);
+    kp = std::max(1, std::min(kp, p.chunks / 4));
+  }
+  p.kp = std::max(1, std::min(kp, p.chunks));
+  if (p.n_blocks > kMaxCounters) p.kp = 1;
+  p.xcd_map = (p.n_blocks % 8 == 0) ? 1 : 0;
+  p.grid_x = p.n_blocks * p.kp;
+  p.ws_bytes = p.kp > 1 ? kCounterBytes + (size_t)p.kp * (size_t)M * (size_t)N * 4u : 0;
+  return DFMI_OK;
+}
+
+template <typename Tag, int GS, int MT>
+static void launch_stream_t(const StreamPlan& p, hipStream_t st, const StreamArgs& a) {
+  const int lds = Stream<Tag, GS, MT>::LDS_BYTES;
+  hipLaunchKernelGGL((qmm_stream_kernel<Tag, GS, MT>), dim3(p.grid_x), dim3(kStreamThreads), lds,
+                     st, a);
+}
+
+template <typename Tag, int GS>
+static void launch_stream_gs(const StreamPlan& p, hipStream_t st, const StreamArgs& a) {
+  if (p.MT == 1) launch_stream_t<Tag, GS, 1>(p, st, a);
+  else launch_stream_t<Tag, GS, 2>(p, st, a);
+}
+
+template <typename Tag>
+static void launch_stream(int gs, const StreamPlan& p, hipStream_t st, const StreamArgs& a) {
+  if (gs == 32) launch_stream_gs<Tag, 32>(p, st, a);
+  else if (gs == 64) launch_stream_gs<Tag, 64>(p, st, a);
+  else launch_stream_gs<Tag, 128>(p, st, a);
+}
+
+// Dynamic LDS above 64 KiB needs the per-kernel attribute raised once.
+template <typename Tag, int GS, int MT>
+static void allow_lds_t() {
+  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&qmm_stream_kernel<Tag, GS, MT>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize,
+                            Stream<Tag, GS, MT>::LDS_BYTES);
+}
+
+template <typename Tag, int GS>
+static void allow_lds_gs() {
+  allow_lds_t<Tag, GS, 1>();
+  allow_lds_t<Tag, GS, 2>();
+}
+
+static void allow_lds_all() {
+  static bool done = false;  // benign race: the attribute calls are idempotent
+  if (done) return;
+  allow_lds_gs<BF16, 32>();
+  allow_lds_gs<BF16, 64>();
+  allow_lds_gs<BF16, 128>();
+  allow_lds_gs<F16, 32>();
+  allow_lds_gs<F16, 64>();
+  allow_lds_gs<F16, 128>();
+  done = true;
 }
 
 static int validate_qmm(int x_dtype, int64_t M, int64_t K, int64_t N, int gs, int bits) {
@@ -248,11 +367,22 @@ static int validate_qmm(int x_dtype, int64_t M, int64_t K, int64_t N, int gs, in
 
 using namespace dfmi;
 
+// Automatic choice (measured on MI355X): the streaming kernel wins once a
+// call has enough weight rows (N >= 8192) or a long enough K (>= 8192) to
+// keep its pipeline full; smaller calls go to the general kernel.
+static bool use_stream(int64_t M, int64_t K, int64_t N, int gs, const dfmi_qmm_tuning* tune) {
+  const int path = tune ? tune->path : 0;
+  if (path == 1 || !stream_eligible(M, K, gs)) return false;
+  if (path == 2) return true;
+  return N >= 8192 || K >= 8192;
+}
+
 extern "C" size_t dfmi_qmm_workspace_bytes_ex(int64_t M, int64_t K, int64_t N, int group_size,
                                               int bits, const dfmi_qmm_tuning* tuning) {
   if (validate_qmm(DFMI_BF16, M, K, N, group_size, bits) != DFMI_OK || M == 0 || N == 0) return 0;
-  DensePlan p;
-  if (plan_dense(M, K, N, tuning, p) != DFMI_OK) return 0;
+  if (!use_stream(M, K, N, group_size, tuning)) return 0;
+  StreamPlan p;
+  if (plan_stream(M, K, N, group_size, tuning, p) != DFMI_OK) return 0;
   return p.ws_bytes;
 }
 
@@ -277,6 +407,45 @@ extern "C" int dfmi_qmm_affine_ex(const void* x, int x_dtype, const uint32_t* w_
     set_error("dfmi_qmm: x, w_q, scales and biases must be 16-byte aligned");
     return DFMI_EINVAL;
   }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (tuning && tuning->path == 2 && !stream_eligible(M, K, group_size)) {
+    set_error("dfmi_qmm: shape M=%lld K=%lld gs=%d outside the streaming kernel", (long long)M,
+              (long long)K, group_size);
+    return DFMI_EINVAL;
+  }
+  if (use_stream(M, K, N, group_size, tuning)) {
+    StreamPlan p;
+    rc = plan_stream(M, K, N, group_size, tuning, p);
+    if (rc != DFMI_OK) return rc;
+    StreamArgs a;
+    a.x = static_cast<const uint16_t*>(x);
+    a.w = w_q;
+    a.s = static_cast<const uint16_t*>(scales);
+    a.b = static_cast<const uint16_t*>(biases);
+    a.y = static_cast<uint16_t*>(y);
+    a.partials = nullptr;
+    a.counters = nullptr;
+    if (p.kp > 1) {
+      if (!workspace || workspace_bytes < p.ws_bytes || !aligned16(workspace)) {
+        set_error("dfmi_qmm: workspace of %zu bytes (16-byte aligned) required, got %zu",
+                  p.ws_bytes, workspace_bytes);
+        return DFMI_ENOSPC;
+      }
+      a.counters = static_cast<uint32_t*>(workspace);
+      a.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
+    }
+    a.M = (int)M;
+    a.K = (int)K;
+    a.N = (int)N;
+    a.chunks = p.chunks;
+    a.kp = p.kp;
+    a.n_blocks = p.n_blocks;
+    a.xcd_map = p.xcd_map;
+    allow_lds_all();
+    if (x_dtype == DFMI_BF16) launch_stream<BF16>(group_size, p, st, a);
+    else launch_stream<F16>(group_size, p, st, a);
+    return check_launch("dfmi_qmm_affine");
+  }
   DensePlan p;
   rc = plan_dense(M, K, N, tuning, p);
   if (rc != DFMI_OK) return rc;
@@ -286,25 +455,10 @@ extern "C" int dfmi_qmm_affine_ex(const void* x, int x_dtype, const uint32_t* w_
   a.s = static_cast<const uint16_t*>(scales);
   a.b = static_cast<const uint16_t*>(biases);
   a.y = static_cast<uint16_t*>(y);
-  a.partials = nullptr;
-  a.counters = nullptr;
-  if (p.kpg > 1) {
-    if (!workspace || workspace_bytes < p.ws_bytes || !aligned16(workspace)) {
-      set_error("dfmi_qmm: workspace of %zu bytes (16-byte aligned) required, got %zu",
-                p.ws_bytes, workspace_bytes);
-      return DFMI_ENOSPC;
-    }
-    a.counters = static_cast<uint32_t*>(workspace);
-    a.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + p.counters_bytes);
-  }
   a.M = (int)M;
   a.K = (int)K;
   a.N = (int)N;
-  a.kpg = p.kpg;
   a.chunks = p.chunks;
-  a.n_blocks = p.n_blocks;
-  a.xcd_map = p.xcd_map;
-  hipStream_t st = static_cast<hipStream_t>(stream);
   if (x_dtype == DFMI_BF16) launch_tag<BF16>(group_size, p, st, a);
   else launch_tag<F16>(group_size, p, st, a);
   return check_launch("dfmi_qmm_affine");

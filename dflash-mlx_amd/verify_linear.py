@@ -26,6 +26,7 @@ from .internal_debug import (
 from .quantize import quantize
 from .verify_qmm import (
     _auto_variant,
+    _tuning,
     _m4_ksplit_np_shape,
     _resolve_m16_ktmpl_variant,
     qmm_launch,
@@ -170,7 +171,7 @@ def _build_dispatch(obj: VerifyQuantizedLinear, *, enable_qmm: Optional[bool] = 
         variant, k_parts = _auto_variant(K, N)
         if variant == "mma2big_pipe" and K % (32 * k_parts) != 0:
             variant, k_parts = "mma2big", 1
-        m16_tuning = _lib.QmmTuning(0, k_parts if variant == "mma2big_pipe" else 1)
+        m16_tuning = _tuning(k_parts if variant == "mma2big_pipe" else 1)
 
     def _stock(x):
         return quantized_matmul(x, obj.weight, obj.scales, obj.biases, transpose=True,

@@ -7,8 +7,8 @@ mma2big_pipe variants, the M=4 k-split variant and the "stock" fallback that
 the reference hands to ``mx.quantized_matmul`` -- runs the same hand-written
 gfx950 kernel family in libdfmi.so (``dfmi_qmm_affine``).  The route only
 selects the launch shape: the reference's ``K_PARTS`` becomes the number of
-workgroups that split K (``DFLASH_VERIFY_QMM_KPARTS`` keeps its meaning), the
-others use the automatic shape.  All shapes compute the same sums in fp32 and
+K splits (``DFLASH_VERIFY_QMM_KPARTS`` keeps its meaning), the others use the
+automatic shape.  All shapes compute the same sums in fp32 and
 differ only in fp32 summation order.
 
 Tensors: ``x`` bf16/f16 ``[..., K]`` on the GPU; ``w`` int32/uint32 words
@@ -82,10 +82,14 @@ def _resolve_m16_ktmpl_variant(K: int, N: int, bits: int,
     return None
 
 
-def _tuning(k_splits: int = 0, tiles_per_wave: int = 0):
-    if not k_splits and not tiles_per_wave:
+def _tuning(k_parts: int = 0):
+    """Launch-shape hint from the reference's K_PARTS: the number of K splits
+    (workgroups on the streaming kernel, wavefronts on the general one, at
+    most 8); 0 means automatic."""
+    if not k_parts:
         return None
-    return _lib.QmmTuning(int(tiles_per_wave), int(k_splits))
+    kp = max(1, min(8, int(k_parts)))
+    return _lib.QmmTuning(0, 0, kp, kp)
 
 
 def qmm_launch(x2: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
@@ -174,10 +178,10 @@ def verify_route(M: int, K: int, N: int, bits: int,
     if selected == "mma2big_pipe":
         if N % 32 != 0 or k_parts <= 0 or K % (32 * k_parts) != 0:
             return "stock", None
-        return "mma2big_pipe", _tuning(k_splits=k_parts)
+        return "mma2big_pipe", _tuning(k_parts)
     if N % 32 != 0 or K % 32 != 0:
         return "stock", None
-    return "mma2big", _tuning(k_splits=1)
+    return "mma2big", _tuning(1)
 
 
 def verify_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,

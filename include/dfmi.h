@@ -19,9 +19,7 @@
  * buffer must be zero-filled once when it is created; the kernels leave every
  * counter and key they use back at zero when they finish, so one workspace
  * serves any sequence of calls on ONE stream.  Calls that overlap in time
- * (different streams) must not share a workspace, and the qmm family and the
- * greedy family (greedy / lm_head) each need their own: each lays out its own
- * counters (the qmm workspace starts with a fixed 64 KiB counter region).
+ * (different streams) must not share a workspace.
  */
 #ifndef DFMI_H
 #define DFMI_H
@@ -49,10 +47,18 @@ const char *dfmi_version(void);
 const char *dfmi_last_error(void);
 
 /* Optional launch-shape override for the affine qmm (tuning sweeps).  Zero
- * fields mean "automatic".  tiles_per_wave: 16-row weight tiles per wavefront
- * (1 or 2); k_splits: workgroups sharing one output block along K. */
+ * fields mean "automatic".
+ *   path: 1 = general kernel, 2 = streaming kernel (DFMI_EINVAL if the shape
+ *         is outside it: M <= 32, K % 256 == 0, K % (8*group_size) == 0);
+ *   tiles_per_wave: general kernel, 16-row weight tiles per wavefront (1, 2,
+ *         4; the streaming kernel always covers 64 rows per workgroup);
+ *   waves_per_block: general kernel, wavefronts of a workgroup that split K
+ *         (1..8; the reference's K_PARTS);
+ *   k_splits: streaming kernel, workgroups that split K of one output block. */
 typedef struct dfmi_qmm_tuning {
+  int path;
   int tiles_per_wave;
+  int waves_per_block;
   int k_splits;
 } dfmi_qmm_tuning;
 
@@ -71,7 +77,10 @@ typedef struct dfmi_qmm_tuning {
  * Supported: bits == 4, group_size in {32, 64, 128}, K % 32 == 0,
  * K % group_size == 0, any M >= 1, any N >= 1; 16-byte aligned x / w_q /
  * scales / biases.  fp32 accumulation, output rounded to nearest even.
- * Anything else returns DFMI_EINVAL without launching.
+ * Anything else returns DFMI_EINVAL without launching.  Results do not depend
+ * on scheduling: every K split is summed in a fixed order.  Shapes that split
+ * K across workgroups need the workspace dfmi_qmm_workspace_bytes reports
+ * (0 bytes -> workspace may be NULL); it must be zero-filled when created.
  */
 int dfmi_qmm_affine(const void *x, int x_dtype, const uint32_t *w_q, const void *scales,
                     const void *biases, void *y, int64_t M, int64_t K, int64_t N,

@@ -117,29 +117,44 @@ def test_closed_form_exact(dev):
         xf[m, idx] = rng.choice([-1.0, 1.0], size=6)
     x = oracle.f32_to_bf16_bits(xf)
     want = oracle.quantized_matmul(x, w_q, s, b, group_size=gs, out_dtype="bf16")
-    for tuning in (None, (1, 1), (2, 4), (1, 4)):
+    for tuning in (None, (1, 1, 1, 0), (1, 2, 4, 0), (1, 4, 8, 0), (1, 1, 3, 0), (2, 1, 0, 1),
+                   (2, 2, 0, 1), (2, 1, 0, 3), (2, 2, 0, 2)):
         got = _run(dev, x, w_q, s, b, gs, tuning=_tuning(tuning))
         assert np.array_equal(got, want), f"tuning {tuning}"
 
 
 def _tuning(t):
+    """(path, tiles_per_wave, waves_per_block, k_splits); path 1 general, 2 streaming."""
     if t is None:
         return None
     from dflash_mlx_amd import _lib
 
-    return _lib.QmmTuning(t[0], t[1])
+    return _lib.QmmTuning(*t)
 
 
-@pytest.mark.parametrize("tiles,splits", [(1, 1), (2, 1), (1, 2), (2, 3), (1, 8), (2, 16)])
-def test_launch_shapes_agree(dev, tiles, splits):
+@pytest.mark.parametrize("tuning", [(1, 1, 1, 0), (1, 2, 1, 0), (1, 1, 2, 0), (1, 2, 3, 0),
+                                    (1, 1, 8, 0), (1, 4, 8, 0), (1, 4, 5, 0),
+                                    (2, 1, 0, 1), (2, 2, 0, 1), (2, 1, 0, 2), (2, 1, 0, 5),
+                                    (2, 2, 0, 4), (2, 1, 0, 16)])
+def test_launch_shapes_agree(dev, tuning):
     x, w_q, s, b = make_qmm_case(16, 4096, 2048, 64, seed=77)
-    got = _run(dev, x, w_q, s, b, 64, tuning=_tuning((tiles, splits)))
+    got = _run(dev, x, w_q, s, b, 64, tuning=_tuning(tuning))
     _check(got, x, w_q, s, b, 64)
 
 
+@pytest.mark.parametrize("M", [1, 8, 16, 24, 32])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+def test_streaming_kernel_shapes(dev, M, gs):
+    # forced onto the streaming kernel, with and without a K split
+    K, N = 2048, 640
+    x, w_q, s, b = make_qmm_case(M, K, N, gs, seed=M * 3 + gs)
+    for t in ((2, 0, 0, 1), (2, 0, 0, 3), (2, 2, 0, 2)):
+        _check(_run(dev, x, w_q, s, b, gs, tuning=_tuning(t)), x, w_q, s, b, gs)
+
+
 def test_deterministic_and_workspace_reuse(dev):
-    # The K-split reduction sums partials in split order, so repeated calls are
-    # bit-identical; interleaving other shapes must not disturb the counters.
+    # The K-split reduction sums the wavefronts' partials in a fixed order, so
+    # repeated calls are bit-identical, whatever ran in between.
     x, w_q, s, b = make_qmm_case(16, 4096, 4096, 64, seed=5)
     x2, w2, s2, b2 = make_qmm_case(16, 5120, 1024, 64, seed=6)
     first = _run(dev, x, w_q, s, b, 64)
