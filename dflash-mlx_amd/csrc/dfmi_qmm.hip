@@ -157,9 +157,10 @@ struct StreamArgs {
   int xcd_map;
 };
 
-template <typename Tag, int GS, int MT>
-__global__ __launch_bounds__(kStreamThreads) void qmm_stream_kernel(StreamArgs a) {
-  using S = Stream<Tag, GS, MT>;
+template <typename Tag, int GS, int MT, int WV>
+__global__ __launch_bounds__(64 * WV) void qmm_stream_kernel(StreamArgs a) {
+  using S = Stream<Tag, GS, MT, WV>;
+  constexpr int kThreads = 64 * WV;
   int nb, kpi;
   {
     const int L = blockIdx.x;
@@ -178,10 +179,10 @@ __global__ __launch_bounds__(kStreamThreads) void qmm_stream_kernel(StreamArgs a
   }
   if (nb >= a.n_blocks) return;  // uniform, before any barrier
   typename S::Ctx cx;
-  cx.x = a.x;
-  cx.w = a.w;
-  cx.s = a.s;
-  cx.b = a.b;
+  cx.x = buffer_rsrc(a.x, (uint32_t)a.M * (uint32_t)a.K * 2u);
+  cx.w = buffer_rsrc(a.w, (uint32_t)a.N * (uint32_t)(a.K / 2));
+  cx.s = buffer_rsrc(a.s, (uint32_t)a.N * (uint32_t)(a.K / GS) * 2u);
+  cx.b = buffer_rsrc(a.b, (uint32_t)a.N * (uint32_t)(a.K / GS) * 2u);
   cx.K = a.K;
   cx.M = a.M;
   cx.N = a.N;
@@ -198,7 +199,7 @@ __global__ __launch_bounds__(kStreamThreads) void qmm_stream_kernel(StreamArgs a
     for (int mt = 0; mt < MT; ++mt) acc[t][mt] = zero4();
   S::run(cx, c0, c1, acc);
 
-  // sum the 4 wavefronts' partial tiles through LDS (the stages are free:
+  // sum the WV wavefronts' partial tiles through LDS (the stages are free:
   // every DMA has landed and every wavefront is past its last LDS read)
   __syncthreads();
   float* red = reinterpret_cast<float*>(dfmi_smem);
@@ -212,13 +213,16 @@ __global__ __launch_bounds__(kStreamThreads) void qmm_stream_kernel(StreamArgs a
         for (int j = 0; j < 4; ++j) mine[((t * MT + mt) * 4 + j) * 64 + cx.lane] = acc[t][mt][j];
   }
   __syncthreads();
-  constexpr int PER = S::RED_FLOATS / kStreamThreads;
+  constexpr int PER = S::RED_FLOATS / kThreads;
   float v[PER];
   int mi[PER], ni[PER];
 #pragma unroll
   for (int q = 0; q < PER; ++q) {
-    const int e = q * kStreamThreads + threadIdx.x;
-    v[q] = red[e] + red[S::RED_FLOATS + e] + red[2 * S::RED_FLOATS + e] + red[3 * S::RED_FLOATS + e];
+    const int e = q * kThreads + threadIdx.x;
+    float sum = red[e];
+#pragma unroll
+    for (int wv = 1; wv < WV; ++wv) sum += red[wv * S::RED_FLOATS + e];
+    v[q] = sum;
     const int l = e & 63, j = (e >> 6) & 3, tm = e >> 8;
     ni[q] = cx.n0 + (tm / MT) * 16 + (l & 15);
     mi[q] = (tm % MT) * 16 + 4 * (l >> 4) + j;
@@ -244,7 +248,7 @@ __global__ __launch_bounds__(kStreamThreads) void qmm_stream_kernel(StreamArgs a
   }
   stage_barrier<0>();
   if (!*s_last) return;
-  for (int idx = threadIdx.x; idx < a.M * S::NB; idx += kStreamThreads) {
+  for (int idx = threadIdx.x; idx < a.M * S::NB; idx += kThreads) {
     const int m = idx / S::NB, n = cx.n0 + idx % S::NB;
     if (n < a.N) {
       float sum = 0.f;
@@ -259,48 +263,64 @@ __global__ __launch_bounds__(kStreamThreads) void qmm_stream_kernel(StreamArgs a
 }
 
 struct StreamPlan {
-  int MT, kp, chunks, n_blocks, grid_x, xcd_map, lds;
+  int MT, WV, kp, chunks, n_blocks, grid_x, xcd_map, lds;
   size_t ws_bytes;
 };
 
-static bool stream_eligible(int64_t M, int64_t K, int gs) {
-  return M <= 32 && K % kChunkK == 0 && K % (8 * gs) == 0;
+// (buffer offsets are 32-bit and the record count a signed int: the packed
+// weights must stay under 2 GiB)
+static bool stream_eligible(int64_t M, int64_t K, int64_t N, int gs) {
+  return M <= 32 && K % 256 == 0 && K % (8 * gs) == 0 && K < (1ll << 24) &&
+         N * (K / 2) < (1ll << 31);
+}
+
+// 8 wavefronts (512-k steps, two wavefronts per SIMD, one workgroup per CU)
+// when K allows and the grid fits on the 256 CUs at once; else 4 wavefronts
+// (two workgroups per CU).
+static int stream_waves(int64_t M, int64_t K, int grid) {
+  return (M <= 16 && K % 512 == 0 && grid <= 256) ? 8 : 4;
 }
 
 static int plan_stream(int64_t M, int64_t K, int64_t N, int gs, const dfmi_qmm_tuning* tune,
                        StreamPlan& p) {
   (void)gs;
   p.MT = M <= 16 ? 1 : 2;
-  p.chunks = (int)(K / kChunkK);
   p.n_blocks = (int)((N + kStreamRows - 1) / kStreamRows);
   int kp;
   if (tune && tune->k_splits > 0) {
     kp = tune->k_splits;
   } else {
-    // one workgroup per CU on 256 CUs, at least 4 chunks per split (every
-    // split pays a pipeline fill and the partial-sum epilogue)
+    // one workgroup per CU on 256 CUs, at least 4 steps of 256 k per split
+    // (every split pays a pipeline fill and the partial-sum epilogue)
     kp = (int)std::lround(256.0 / (double)p.n_blocks);
-    kp = std::max(1, std::min(kp, p.chunks / 4));
+    kp = std::max(1, std::min(kp, (int)(K / 1024)));
   }
-  p.kp = std::max(1, std::min(kp, p.chunks));
+  p.kp = std::max(1, std::min(kp, (int)(K / 256)));
   if (p.n_blocks > kMaxCounters) p.kp = 1;
+  p.WV = stream_waves(M, K, p.n_blocks * p.kp);
+  p.chunks = (int)(K / (64 * p.WV));
+  p.kp = std::min(p.kp, p.chunks);
   p.xcd_map = (p.n_blocks % 8 == 0) ? 1 : 0;
   p.grid_x = p.n_blocks * p.kp;
   p.ws_bytes = p.kp > 1 ? kCounterBytes + (size_t)p.kp * (size_t)M * (size_t)N * 4u : 0;
   return DFMI_OK;
 }
 
-template <typename Tag, int GS, int MT>
+template <typename Tag, int GS, int MT, int WV>
 static void launch_stream_t(const StreamPlan& p, hipStream_t st, const StreamArgs& a) {
-  const int lds = Stream<Tag, GS, MT>::LDS_BYTES;
-  hipLaunchKernelGGL((qmm_stream_kernel<Tag, GS, MT>), dim3(p.grid_x), dim3(kStreamThreads), lds,
+  const int lds = Stream<Tag, GS, MT, WV>::LDS_BYTES;
+  hipLaunchKernelGGL((qmm_stream_kernel<Tag, GS, MT, WV>), dim3(p.grid_x), dim3(64 * WV), lds,
                      st, a);
 }
 
 template <typename Tag, int GS>
 static void launch_stream_gs(const StreamPlan& p, hipStream_t st, const StreamArgs& a) {
-  if (p.MT == 1) launch_stream_t<Tag, GS, 1>(p, st, a);
-  else launch_stream_t<Tag, GS, 2>(p, st, a);
+  if (p.MT == 1) {
+    if (p.WV == 8) launch_stream_t<Tag, GS, 1, 8>(p, st, a);
+    else launch_stream_t<Tag, GS, 1, 4>(p, st, a);
+  } else {
+    launch_stream_t<Tag, GS, 2, 4>(p, st, a);
+  }
 }
 
 template <typename Tag>
@@ -311,17 +331,18 @@ static void launch_stream(int gs, const StreamPlan& p, hipStream_t st, const Str
 }
 
 // Dynamic LDS above 64 KiB needs the per-kernel attribute raised once.
-template <typename Tag, int GS, int MT>
+template <typename Tag, int GS, int MT, int WV>
 static void allow_lds_t() {
-  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&qmm_stream_kernel<Tag, GS, MT>),
+  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&qmm_stream_kernel<Tag, GS, MT, WV>),
                             hipFuncAttributeMaxDynamicSharedMemorySize,
-                            Stream<Tag, GS, MT>::LDS_BYTES);
+                            Stream<Tag, GS, MT, WV>::LDS_BYTES);
 }
 
 template <typename Tag, int GS>
 static void allow_lds_gs() {
-  allow_lds_t<Tag, GS, 1>();
-  allow_lds_t<Tag, GS, 2>();
+  allow_lds_t<Tag, GS, 1, 4>();
+  allow_lds_t<Tag, GS, 1, 8>();
+  allow_lds_t<Tag, GS, 2, 4>();
 }
 
 static void allow_lds_all() {
@@ -372,7 +393,7 @@ using namespace dfmi;
 // keep its pipeline full; smaller calls go to the general kernel.
 static bool use_stream(int64_t M, int64_t K, int64_t N, int gs, const dfmi_qmm_tuning* tune) {
   const int path = tune ? tune->path : 0;
-  if (path == 1 || !stream_eligible(M, K, gs)) return false;
+  if (path == 1 || !stream_eligible(M, K, N, gs)) return false;
   if (path == 2) return true;
   return N >= 8192 || K >= 8192;
 }
@@ -408,7 +429,7 @@ extern "C" int dfmi_qmm_affine_ex(const void* x, int x_dtype, const uint32_t* w_
     return DFMI_EINVAL;
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (tuning && tuning->path == 2 && !stream_eligible(M, K, group_size)) {
+  if (tuning && tuning->path == 2 && !stream_eligible(M, K, N, group_size)) {
     set_error("dfmi_qmm: shape M=%lld K=%lld gs=%d outside the streaming kernel", (long long)M,
               (long long)K, group_size);
     return DFMI_EINVAL;

@@ -1,18 +1,24 @@
 // Streaming main loop of the verify-path matmuls (fast path).
 //
-// A workgroup of 4 wavefronts owns a block of NB = 64 weight rows (four
-// 16-row MFMA tiles) and a range of K chunks (256 k = 128 bytes of every
-// int4 weight row).  Cost model (measured on MI355X):
+// A workgroup of WV (4 or 8) wavefronts owns a block of NB = 64 weight rows
+// (four 16-row MFMA tiles) and a range of K steps of CK = 64*WV k.  Cost
+// model (measured on MI355X):
 //
 //   * a CU's vector memory pipeline retires roughly one cache-line request
 //     every few cycles however few bytes of the line an instruction uses, so
-//     every global read is a whole-line request: weights (8 rows x 128 B per
-//     instruction), activations (2 rows x 512 B) and scales / biases
-//     (8 rows x 64 B of each array) go straight to LDS with
-//     global_load_lds_dwordx4, kDepth chunks ahead;
+//     every global read is a whole-line request: weights (whole 32*WV-byte
+//     row pieces), activations (whole rows) and scales / biases (8 rows x
+//     64 B of each array) go straight to LDS with global_load_lds_dwordx4,
+//     kDepth steps ahead;
+//   * the loop is VALU-issue bound (a SIMD retires one wave64 VALU op per
+//     ~4.2 cycles), so every address is computed once per lane: a DMA is an
+//     SGPR base (advanced by scalar adds) plus a lane-constant VGPR offset,
+//     and the fragment reads of a step cost one VGPR add per LDS region, the
+//     rest being immediate offsets;
 //   * LDS read latency is hidden by register double buffering: the fragments
-//     of chunk c+1 are read from LDS while chunk c is computed;
-//   * each wavefront takes a 64-k slice of every chunk for all four tiles, so
+//     of step c+1 are read from LDS while step c is computed, and WV = 8 puts
+//     two wavefronts on every SIMD to overlap the remaining stalls;
+//   * each wavefront takes a 64-k slice of every step for all four tiles, so
 //     the activation stage is read from LDS once per workgroup (not once per
 //     wavefront) and its group sums cost two MFMAs per slice;
 //   * every LDS layout is XOR-swizzled per row so the fragment reads spread
@@ -30,7 +36,7 @@
 // Synchronisation: LDS DMA loads are tracked by vmcnt only, and the compiler
 // does not know that a later ds_read depends on them, so the loop waits with
 // an explicit s_waitcnt vmcnt(n) (n = loads this wavefront issued after the
-// chunk it needs) followed by a workgroup barrier, once per chunk.  The same
+// step it needs) followed by a workgroup barrier, once per step.  The same
 // barrier (with lgkmcnt(0)) proves that every wavefront has finished reading
 // the stage the next DMA overwrites.
 #pragma once
@@ -39,8 +45,6 @@
 
 namespace dfmi {
 
-constexpr int kStreamWaves = 4;
-constexpr int kStreamThreads = kStreamWaves * 64;
 constexpr int kStreamRows = 64;   // weight rows per workgroup
 constexpr int kStreamTiles = 4;   // 16-row MFMA tiles per workgroup, all in every wavefront
 constexpr int kDepth = 3;         // LDS stages
@@ -64,48 +68,86 @@ __device__ inline void stage_barrier() {
 // Dynamic LDS of the streaming kernels (one allocation per workgroup).
 extern __shared__ __attribute__((aligned(16))) char dfmi_smem[];
 
-__device__ inline void dma16(const void* g, void* lds_uniform) {
-  __builtin_amdgcn_global_load_lds(const_cast<void*>(g), lds_uniform, 16, 0, 0);
+// Raw buffer resource over [base, base + bytes): word 3 = 0x00020000 (32-bit
+// data format, the gfx9 raw-buffer setting); reads at or past `bytes` return
+// zero instead of touching memory.
+__device__ inline __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
 }
 
-template <typename Tag, int GS, int MT>
+// 16 bytes per lane from a buffer (lane-constant VGPR offset + wave-uniform
+// SGPR offset: no vector arithmetic per load) to LDS (wave-uniform
+// destination; lane l lands at dst + 16 l).
+typedef __attribute__((address_space(3))) void lds_void;
+__device__ inline void dma16(__amdgpu_buffer_rsrc_t rsrc, uint32_t lane_off, uint32_t uni_off,
+                             char* lds_uniform) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)lds_uniform, 16, lane_off, uni_off, 0,
+                                           0);
+}
+
+// A wave-uniform value the compiler may not split into constant parts (so a
+// region base stays in one SGPR and the per-tile offsets fit the 16-bit
+// ds_read immediate).
+__device__ inline uint32_t opaque(uint32_t v) {
+  asm volatile("" : "+s"(v));
+  return v;
+}
+
+template <typename Tag, int GS, int MT, int WV>
 struct Stream {
   static constexpr int NT = kStreamTiles;
   static constexpr int NB = kStreamRows;
-  static constexpr int GPC = kChunkK / GS;  // quantisation groups per chunk
-  static constexpr int SBC = 32 / GPC;      // chunks per scale / bias block (32 groups)
+  static constexpr int CK = 64 * WV;        // k per step
+  static constexpr int GPC = CK / GS;       // quantisation groups per step
+  static constexpr int SBC = 32 / GPC;      // steps per scale / bias block (32 groups)
+  static constexpr int XROW = CK * 2;       // bytes of one activation row per step
+  static constexpr int XPPR = CK / 8;       // 16-byte pieces per activation row
+  static constexpr int WROW = CK / 2;       // bytes of one weight row per step
+  static constexpr int WPPR = WROW / 16;    // 16-byte pieces per weight row
+  static_assert(WV == 4 || WV == 8, "wavefronts");
+  static_assert(SBC >= 2, "scale block reuse distance");
   // gs >= 64: a lane's two k-blocks take adjacent words (one 8-byte LDS read);
   // gs = 32: k-block j is group 2*wave + j, so the blocks stay group-pure.
   static constexpr bool PAIR = GS >= 64;
-  static constexpr int XBUF = MT * 16 * 512;  // bytes of one activation stage
-  static constexpr int WBUF = NB * 128;       // bytes of one weight stage
-  static constexpr int SBBUF = NB * 128;      // per row: 64 B of scales, then 64 B of biases
-  static constexpr int X_OFF = 0;
-  static constexpr int W_OFF = kDepth * XBUF;
-  static constexpr int SB_OFF = W_OFF + kDepth * WBUF;
-  static constexpr int LDS_BYTES = SB_OFF + 2 * SBBUF;
+  static constexpr int XBUF = MT * 16 * XROW;  // bytes of one activation stage
+  static constexpr int WBUF = NB * WROW;       // bytes of one weight stage
+  static constexpr int SBBUF = NB * 128;       // 64 B of scales per row, then 64 B of biases per row
+  // Scale / bias buffers first: their fragment reads use immediate offsets
+  // (the ds_read offset field is 16 bits).
+  static constexpr int SB_OFF = 0;
+  static constexpr int X_OFF = 2 * SBBUF;
+  static constexpr int W_OFF = X_OFF + kDepth * XBUF;
+  static constexpr int LDS_BYTES = W_OFF + kDepth * WBUF;
   // epilogue: [wave][t][mt][reg][lane] floats, aliasing the stages
   static constexpr int RED_FLOATS = NT * MT * 4 * 64;
-  static_assert(kStreamWaves * RED_FLOATS * 4 <= LDS_BYTES, "reduction buffer");
-  // DMA instructions per wavefront
-  static constexpr int X_DMA = MT * 2;  // MT*16 rows x 512 B per stage / 4 waves / 1 KiB
-  static constexpr int W_DMA = 2;       // 64 rows x 128 B / 4 waves / 1 KiB
-  static constexpr int SB_DMA = 2;      // 64 rows x 128 B per block / 4 waves / 1 KiB
+  static_assert(WV * RED_FLOATS * 4 <= LDS_BYTES, "reduction buffer");
+  // DMA instructions (1 KiB each) per wavefront
+  static constexpr int X_DMA = XBUF / 1024 / WV;    // = 2 * MT
+  static constexpr int W_DMA = WBUF / 1024 / WV;    // = 2
+  static constexpr int SB_DMA = SBBUF / 1024 / WV;  // 2 (WV = 4) or 1 (WV = 8)
   static constexpr int CHUNK_DMA = X_DMA + W_DMA;
   static_assert(GS == 32 || GS == 64 || GS == 128, "group size");
 
   struct Ctx {
-    const uint16_t* x;
-    const uint32_t* w;
-    const uint16_t* s;
-    const uint16_t* b;
+    __amdgpu_buffer_rsrc_t x, w, s, b;  // activations, packed weights, scales, biases
     int K, M, N;
     int groups;  // K / GS
     int n0;      // first weight row of this workgroup
     int wave, lane;
   };
 
-  // One chunk's operands of this lane, read from LDS.
+  // Lane-constant offsets, computed once.
+  struct Lane {
+    uint32_t xg[X_DMA];  // activation DMA: byte offset in x of this lane's piece at step 0
+    uint32_t wg[W_DMA];  // weight DMA: byte offset in w at step 0
+    uint32_t xo[2];      // activation fragment j: byte offset inside a stage (M-block 0)
+    uint32_t wo[2];      // weight fragment (j = 0; j = 1 too at gs = 32): offset inside a stage (tile 0)
+    uint32_t sbl;        // scale fragment: row offset with its swizzle bits (tile 0, buffer 0)
+    uint32_t hsel;       // v_perm selector moving this wavefront's 16-bit half to the high half
+  };
+
+  // One step's operands of this lane, read from LDS.
   struct Frag {
     u32x4 x[MT][2];     // activations of k-block j
     uint32_t w[NT][2];  // packed words of k-block j
@@ -113,116 +155,141 @@ struct Stream {
     uint32_t bv[NT];    // dword holding this lane's bias(es)
   };
 
-  // word (= 8-k piece) of the chunk that lane group kg feeds k-block j with
+  // word (= 8-k piece) of the step that lane group kg feeds k-block j with
   __device__ static inline int piece_of(int wave, int kg, int j) {
     return PAIR ? 8 * wave + 2 * kg + j : 8 * wave + 4 * j + kg;
   }
 
-  // Activation stage: instruction j covers rows 2j, 2j+1; lane l loads piece
-  // (l & 31) ^ (row & 15) of its row into slot l & 31.  Rows >= M re-read
-  // row M-1 (their outputs are never stored).
-  __device__ static inline void issue_x(const Ctx& cx, int c, int stage) {
+  __device__ static inline Lane lane_setup(const Ctx& cx) {
+    Lane L;
+    const int col = cx.lane & 15, kg = cx.lane >> 4;
+    // activation stage: instruction j covers 64 / XPPR consecutive rows; lane
+    // l loads piece (l % XPPR) ^ (row & 15) of its row into slot l % XPPR;
+    // rows >= M re-read row M-1 (their outputs are never stored)
 #pragma unroll
     for (int i = 0; i < X_DMA; ++i) {
       const int j = cx.wave * X_DMA + i;
-      const int r = 2 * j + (cx.lane >> 5);
-      const int slot = cx.lane & 31;
-      const int piece = slot ^ (r & 15);
+      const int r = j * (64 / XPPR) + cx.lane / XPPR;
+      const int piece = (cx.lane % XPPR) ^ (r & 15);
       const int m = min(r, cx.M - 1);
-      const uint16_t* g = cx.x + (int64_t)m * cx.K + c * kChunkK + piece * 8;
-      dma16(g, dfmi_smem + X_OFF + stage * XBUF + j * 1024);
+      L.xg[i] = (uint32_t)m * (uint32_t)cx.K * 2u + (uint32_t)piece * 16u;
     }
-  }
-
-  // Weight stage: instruction i of wavefront w covers rows 8*(2w+i) .. +7;
-  // lane l loads piece (l & 7) ^ (row & 7) of its row into slot l & 7.
-  // Rows >= N re-read row N-1.
-  __device__ static inline void issue_w(const Ctx& cx, int c, int stage) {
-    const uint32_t kw = (uint32_t)(cx.K / 8);
+    // weight stage: instruction i of wavefront w covers 64 / WPPR consecutive
+    // rows; lane l loads piece (l % WPPR) ^ (row % WPPR) of its row into slot
+    // l % WPPR; rows >= N re-read row N-1
+    constexpr int RPI = 64 / WPPR;
 #pragma unroll
     for (int i = 0; i < W_DMA; ++i) {
-      const int r0 = (cx.wave * W_DMA + i) * 8;
-      const int r = r0 + (cx.lane >> 3);
-      const int piece = (cx.lane & 7) ^ (r & 7);
+      const int r = (cx.wave * W_DMA + i) * RPI + cx.lane / WPPR;
+      const int piece = (cx.lane % WPPR) ^ (r % WPPR);
       const int n = min(cx.n0 + r, cx.N - 1);
-      const uint32_t* g = cx.w + (uint32_t)n * kw + (uint32_t)c * 32u + piece * 4;
-      dma16(g, dfmi_smem + W_OFF + stage * WBUF + r0 * 128);
+      L.wg[i] = (uint32_t)n * (uint32_t)(cx.K / 2) + (uint32_t)piece * 16u;
     }
+    // fragment reads (row m = col of M-block 0, row r = col of tile 0; the
+    // other blocks / tiles are whole-row multiples away)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      L.xo[j] = (uint32_t)(col * XROW + ((piece_of(cx.wave, kg, j) ^ col) * 16));
+      const int byte = piece_of(cx.wave, kg, j) * 4;
+      L.wo[j] = (uint32_t)(col * WROW + (((byte >> 4) ^ (col % WPPR)) * 16) + (byte & 15));
+    }
+    L.sbl = (uint32_t)(col * 64 + (((col >> 2) & 3) << 4));
+    const int half = PAIR ? (((cx.wave * 64) / GS) & 1) : 0;
+    L.hsel = half ? 0x03020c0cu : 0x01000c0cu;
+    return L;
   }
 
-  // Scale / bias block sb = groups [32 sb, 32 sb + 32) of every row: per row
-  // 4 pieces of 16 B of each array; lane l of instruction i (rows r0 .. r0+7)
-  // loads array (l >> 2) & 1, piece (l & 3) ^ ((row >> 1) & 3) into slot l & 3.
-  // Pieces past the end of a row re-read its last piece (never used).
+  __device__ static inline void issue_x(const Ctx& cx, const Lane& L, int c, int stage) {
+    const uint32_t u = (uint32_t)c * (uint32_t)(CK * 2);
+#pragma unroll
+    for (int i = 0; i < X_DMA; ++i)
+      dma16(cx.x, L.xg[i], u, dfmi_smem + X_OFF + stage * XBUF + (cx.wave * X_DMA + i) * 1024);
+  }
+
+  __device__ static inline void issue_w(const Ctx& cx, const Lane& L, int c, int stage) {
+    const uint32_t u = (uint32_t)c * (uint32_t)(CK / 2);
+    constexpr int RPI = 64 / WPPR;
+#pragma unroll
+    for (int i = 0; i < W_DMA; ++i)
+      dma16(cx.w, L.wg[i], u,
+            dfmi_smem + W_OFF + stage * WBUF + (cx.wave * W_DMA + i) * RPI * WROW);
+  }
+
+  // Scale / bias block sb = groups [32 sb, 32 sb + 32) of every row, laid
+  // out as [array][row][64 B] (4 pieces of 16 B per row and array).
+  // Instruction j of the workgroup (array j / 4, rows 16 (j % 4) .. +15):
+  // lane l loads piece (l & 3) ^ ((row >> 2) & 3) of row r0 + (l >> 2) into
+  // slot l & 3.  Pieces past the end of a row re-read its last piece (never
+  // used).  Once per SBC steps, so its addresses are computed here.
   __device__ static inline void issue_sb(const Ctx& cx, int sb, int buf) {
     const int last_piece = cx.groups / 8 - 1;  // 8 16-bit values per piece
 #pragma unroll
     for (int i = 0; i < SB_DMA; ++i) {
-      const int r0 = (cx.wave * SB_DMA + i) * 8;
-      const int r = r0 + (cx.lane >> 3);
-      const int arr = (cx.lane >> 2) & 1;
-      const int q = (cx.lane & 3) ^ ((r >> 1) & 3);
+      const int j = cx.wave * SB_DMA + i;  // 0 .. 7, wave-uniform
+      const int arr = j >> 2;
+      const int r0 = (j & 3) * 16;
+      const int r = r0 + (cx.lane >> 2);
+      const int q = (cx.lane & 3) ^ ((r >> 2) & 3);
       const int n = min(cx.n0 + r, cx.N - 1);
       const int piece = min(sb * 4 + q, last_piece);
-      const uint16_t* base = arr ? cx.b : cx.s;
-      const uint16_t* g = base + (int64_t)n * cx.groups + piece * 8;
-      dma16(g, dfmi_smem + SB_OFF + buf * SBBUF + r0 * 128);
+      const uint32_t off = ((uint32_t)n * (uint32_t)cx.groups + (uint32_t)piece * 8u) * 2u;
+      dma16(arr ? cx.b : cx.s, off, 0u, dfmi_smem + SB_OFF + buf * SBBUF + arr * 4096 + r0 * 64);
     }
   }
 
-  __device__ static inline void issue_chunk(const Ctx& cx, int c, int stage) {
-    issue_x(cx, c, stage);
-    issue_w(cx, c, stage);
+  __device__ static inline void issue_chunk(const Ctx& cx, const Lane& L, int c, int stage) {
+    issue_x(cx, L, c, stage);
+    issue_w(cx, L, c, stage);
   }
 
-  // Chunk c's fragments of this lane from LDS stage `stage`, scale buffer sbuf.
-  __device__ static inline void read_frag(const Ctx& cx, int c, int stage, int sbuf, Frag& f) {
-    const int col = cx.lane & 15, kg = cx.lane >> 4;
-    const char* xs = dfmi_smem + X_OFF + stage * XBUF;
+  // Step c's fragments of this lane from LDS stage `stage`, scale buffer sbuf.
+  __device__ static inline void read_frag(const Ctx& cx, const Lane& L, int c, int stage, int sbuf,
+                                          Frag& f) {
+    const uint32_t xb = opaque((uint32_t)(X_OFF + stage * XBUF));
+    const uint32_t wb = opaque((uint32_t)(W_OFF + stage * WBUF));
+    const char* xs0 = dfmi_smem + (L.xo[0] + xb);
+    const char* xs1 = dfmi_smem + (L.xo[1] + xb);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      const int m = mt * 16 + col;
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int slot = piece_of(cx.wave, kg, j) ^ col;
-        f.x[mt][j] = *reinterpret_cast<const u32x4*>(xs + m * 512 + slot * 16);
-      }
+      f.x[mt][0] = *reinterpret_cast<const u32x4*>(xs0 + mt * 16 * XROW);
+      f.x[mt][1] = *reinterpret_cast<const u32x4*>(xs1 + mt * 16 * XROW);
     }
-    const char* ws = dfmi_smem + W_OFF + stage * WBUF;
-    // group index of this lane's first k-block inside the scale / bias block
+    const char* ws0 = dfmi_smem + (L.wo[0] + wb);
+    const char* ws1 = dfmi_smem + (L.wo[1] + wb);
+    // this step's group inside the scale block: byte offset gi*2 of the row's
+    // 64-byte block, as 16-byte piece (swizzled by XOR) and dword offset
     const int gi = (c % SBC) * GPC + (PAIR ? (cx.wave * 64) / GS : 2 * cx.wave);
-    const int sbyte = gi * 2;
+    const uint32_t u = (uint32_t)(sbuf * SBBUF + gi * 2) & ~3u;
+    const char* sbp = dfmi_smem + SB_OFF + (L.sbl ^ u);
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      const int r = t * 16 + col;
-      const char* row = ws + r * 128;
       if constexpr (PAIR) {
-        const int byte = piece_of(cx.wave, kg, 0) * 4;
-        const int slot = (byte >> 4) ^ (r & 7);
-        const u32x2 v = *reinterpret_cast<const u32x2*>(row + slot * 16 + (byte & 15));
+        const u32x2 v = *reinterpret_cast<const u32x2*>(ws0 + t * 16 * WROW);
         f.w[t][0] = v.x;
         f.w[t][1] = v.y;
       } else {
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const int byte = piece_of(cx.wave, kg, j) * 4;
-          const int slot = (byte >> 4) ^ (r & 7);
-          f.w[t][j] = *reinterpret_cast<const uint32_t*>(row + slot * 16 + (byte & 15));
-        }
+        f.w[t][0] = *reinterpret_cast<const uint32_t*>(ws0 + t * 16 * WROW);
+        f.w[t][1] = *reinterpret_cast<const uint32_t*>(ws1 + t * 16 * WROW);
       }
-      const int slot = (sbyte >> 4) ^ ((r >> 1) & 3);
-      const char* p = dfmi_smem + SB_OFF + sbuf * SBBUF + r * 128 + slot * 16 + (sbyte & 12);
-      f.sv[t] = *reinterpret_cast<const uint32_t*>(p);
-      f.bv[t] = *reinterpret_cast<const uint32_t*>(p + 64);
+      f.sv[t] = *reinterpret_cast<const uint32_t*>(sbp + t * 16 * 64);
+      f.bv[t] = *reinterpret_cast<const uint32_t*>(sbp + t * 16 * 64 + 4096);
     }
   }
 
-  // 16-bit value (half 0: low, 1: high) of a packed pair as fp32
-  __device__ static inline float half_of(uint32_t v, int half) {
-    return half ? Num<Tag>::hi(v) : Num<Tag>::lo(v);
+  // 16-bit value of a packed pair as fp32; sel moves the wanted half to the
+  // high half (bf16: that is the fp32 bit pattern)
+  __device__ static inline float half_bf16(uint32_t v, uint32_t sel) {
+    return __uint_as_float(__builtin_amdgcn_perm(v, v, sel));
+  }
+  __device__ static inline float half_of(uint32_t v, uint32_t sel) {
+    if constexpr (std::is_same<Tag, BF16>::value) {
+      return half_bf16(v, sel);
+    } else {
+      return Num<Tag>::hi(__builtin_amdgcn_perm(v, v, sel));
+    }
   }
 
-  __device__ static inline void compute(const Ctx& cx, const Frag& f, f32x4 (&acc)[NT][MT],
+  __device__ static inline void compute(const Lane& L, const Frag& f, f32x4 (&acc)[NT][MT],
                                         const DqConst& dq) {
     const u32x4 ones = u32x4{Num<Tag>::ONE2, Num<Tag>::ONE2, Num<Tag>::ONE2, Num<Tag>::ONE2};
     // group sums of the slice: lane (col, kg) gets X[m = 4 kg + r] in register r
@@ -236,15 +303,13 @@ struct Stream {
         xs[mt][1] = Num<Tag>::mma(f.x[mt][1], ones, zero4());
       }
     }
-    // which half of the scale dword is this wavefront's group (gs >= 64)
-    const int half = PAIR ? (((cx.wave * 64) / GS) & 1) : 0;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       const u32x4 b0 = dequant_word4<Tag>(f.w[t][0], dq);
       const u32x4 b1 = dequant_word4<Tag>(f.w[t][1], dq);
       if constexpr (PAIR) {
-        const float s = half_of(f.sv[t], half);
-        const float bq = __builtin_fmaf(-Num<Tag>::OFF, s, half_of(f.bv[t], half));
+        const float s = half_of(f.sv[t], L.hsel);
+        const float bq = __builtin_fmaf(-Num<Tag>::OFF, s, half_of(f.bv[t], L.hsel));
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
           const f32x4 p = Num<Tag>::mma(f.x[mt][1], b1, Num<Tag>::mma(f.x[mt][0], b0, zero4()));
@@ -255,8 +320,9 @@ struct Stream {
       } else {
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-          const float s = half_of(f.sv[t], j);
-          const float bq = __builtin_fmaf(-Num<Tag>::OFF, s, half_of(f.bv[t], j));
+          const uint32_t sel = j ? 0x03020c0cu : 0x01000c0cu;
+          const float s = half_of(f.sv[t], sel);
+          const float bq = __builtin_fmaf(-Num<Tag>::OFF, s, half_of(f.bv[t], sel));
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) {
             const f32x4 p = Num<Tag>::mma(f.x[mt][j], j ? b1 : b0, zero4());
@@ -270,62 +336,56 @@ struct Stream {
     }
   }
 
-  // Wait for the loads of one chunk: n = loads this wavefront issued after
-  // them (one of 0, C, C+S, 2C, 2C+S with C = CHUNK_DMA, S = SB_DMA).
-  __device__ static inline void wait_chunk(int n) {
-    constexpr int C = CHUNK_DMA, S = SB_DMA;
-    if (n == C) stage_barrier<C>();
-    else if (n == C + S) stage_barrier<C + S>();
-    else if (n == 2 * C) stage_barrier<2 * C>();
-    else if (n == 2 * C + S) stage_barrier<2 * C + S>();
-    else stage_barrier<0>();
-  }
-
-  // loads issued for chunk c (0 when c is past the range end c1)
-  __device__ static inline int loads_of(int c, int c1) {
-    return c < c1 ? CHUNK_DMA + ((c % SBC) == 0 ? SB_DMA : 0) : 0;
-  }
-
-  // iteration c: chunk c+1 must be in LDS; chunk c is in `cur`
-  __device__ static inline void step(const Ctx& cx, int c, int c1, int stage, Frag& cur,
-                                     Frag& nxt, f32x4 (&acc)[NT][MT], const DqConst& dq) {
+  // iteration c: step c+1 must be in LDS; step c is in `cur`.  The wait asks
+  // for at most CHUNK_DMA newer loads (step c+2's activations and weights):
+  // when step c+2 also brought a scale block (issued before them) this
+  // over-waits by that block, which lands with them anyway.
+  __device__ static inline void step(const Ctx& cx, const Lane& L, int c, int c1, int stage,
+                                     Frag& cur, Frag& nxt, f32x4 (&acc)[NT][MT],
+                                     const DqConst& dq) {
     if (c + 1 < c1) {
-      wait_chunk(loads_of(c + 2, c1));
+      if (c + 2 < c1) stage_barrier<CHUNK_DMA>();
+      else stage_barrier<0>();
       if (c + 3 < c1) {
         if ((c + 3) % SBC == 0) issue_sb(cx, (c + 3) / SBC, ((c + 3) / SBC) & 1);
-        issue_chunk(cx, c + 3, stage);  // chunk c's stage: its fragments are in cur
+        issue_chunk(cx, L, c + 3, stage);  // step c's stage: its fragments are in cur
       }
       const int st1 = stage == 2 ? 0 : stage + 1;
-      read_frag(cx, c + 1, st1, ((c + 1) / SBC) & 1, nxt);
+      read_frag(cx, L, c + 1, st1, ((c + 1) / SBC) & 1, nxt);
     }
-    compute(cx, cur, acc, dq);
+    compute(L, cur, acc, dq);
   }
 
-  // Accumulate chunks [c0, c1) (c1 > c0) of this workgroup into acc.  Every
+  // Accumulate steps [c0, c1) (c1 > c0) of this workgroup into acc.  Every
   // wavefront of the workgroup calls this with the same range (it contains
   // barriers).
   __device__ static inline void run(const Ctx& cx, int c0, int c1, f32x4 (&acc)[NT][MT]) {
     const DqConst dq = dq_const<Tag>();
+    const Lane L = lane_setup(cx);
     issue_sb(cx, c0 / SBC, (c0 / SBC) & 1);
-    issue_chunk(cx, c0, 0);
+    issue_chunk(cx, L, c0, 0);
 #pragma unroll
     for (int k = 1; k < kDepth; ++k) {
       if (c0 + k < c1) {
         if ((c0 + k) % SBC == 0) issue_sb(cx, (c0 + k) / SBC, ((c0 + k) / SBC) & 1);
-        issue_chunk(cx, c0 + k, k);
+        issue_chunk(cx, L, c0 + k, k);
       }
     }
-    wait_chunk(loads_of(c0 + 1, c1) + loads_of(c0 + 2, c1));
+    // step c0 in LDS: at most the loads of steps c0+1, c0+2 outstanding
+    // (over-waits by a scale block issued with one of them)
+    if (c0 + 2 < c1) stage_barrier<2 * CHUNK_DMA>();
+    else if (c0 + 1 < c1) stage_barrier<CHUNK_DMA>();
+    else stage_barrier<0>();
     Frag fa, fb;
-    read_frag(cx, c0, 0, (c0 / SBC) & 1, fa);
+    read_frag(cx, L, c0, 0, (c0 / SBC) & 1, fa);
     int c = c0, stage = 0;
     for (; c + 1 < c1; c += 2) {
-      step(cx, c, c1, stage, fa, fb, acc, dq);
+      step(cx, L, c, c1, stage, fa, fb, acc, dq);
       stage = stage == 2 ? 0 : stage + 1;
-      step(cx, c + 1, c1, stage, fb, fa, acc, dq);
+      step(cx, L, c + 1, c1, stage, fb, fa, acc, dq);
       stage = stage == 2 ? 0 : stage + 1;
     }
-    if (c < c1) step(cx, c, c1, stage, fa, fb, acc, dq);
+    if (c < c1) step(cx, L, c, c1, stage, fa, fb, acc, dq);
   }
 };
 
