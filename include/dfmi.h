@@ -103,9 +103,9 @@ size_t dfmi_qmm_workspace_bytes_ex(int64_t M, int64_t K, int64_t N, int group_si
  * QuantizedSwitchLinear (reached from dflash_mlx/engine/target_qwen_gdn.py:865,874),
  * with the lhs broadcast resolved to explicit row ids.  lhs_rows may be NULL
  * (row p for pair p).  Pair order is free (sorted or not); results are
- * per pair.  Expert ids outside [0, E) and row ids outside [0, x_rows) give
- * DFMI_EINVAL (checked on the device: the pair's output row is filled with NaN
- * and the call still returns DFMI_OK -- validate on the host when it matters).
+ * per pair.  Expert ids outside [0, E) and row ids outside [0, x_rows) are
+ * checked on the device: that pair's output row is filled with NaN (the call
+ * still returns DFMI_OK; validate on the host when it matters).  P <= 65535.
  */
 int dfmi_gather_qmm_affine(const void *x, int x_dtype, int64_t x_rows, const uint32_t *w_q,
                            const void *scales, const void *biases, const int32_t *lhs_rows,

@@ -1,0 +1,82 @@
+"""The C ABI (include/dfmi.h) without a GPU: libdfmi.so loads, exports every
+declared function, the ctypes table binds exactly that set, and the host-side
+argument checks answer without touching the device."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from dflash_mlx_amd import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include",
+                      "dfmi.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(dfmi_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_lib.LIB_PATH):
+        import __graft_entry__
+
+        __graft_entry__.build()
+    return _lib.load()
+
+
+def test_header_declares_the_bound_set():
+    declared = _declared()
+    assert declared, "no declarations parsed"
+    assert declared == sorted(_lib.EXPORTED_SYMBOLS)
+
+
+def test_every_declared_symbol_is_exported(lib):
+    raw = ctypes.CDLL(_lib.LIB_PATH)
+    missing = [name for name in _declared() if not hasattr(raw, name)]
+    assert not missing, missing
+    assert _lib.missing_symbols() == []
+
+
+def test_version_and_error_string(lib):
+    assert lib.dfmi_version().decode().startswith("dfmi ")
+    assert isinstance(lib.dfmi_last_error(), bytes)
+
+
+def test_host_side_validation_without_gpu(lib):
+    # bits, group size, dtype and shape checks return DFMI_EINVAL before any device call
+    assert lib.dfmi_qmm_affine(None, _lib.DFMI_BF16, None, None, None, None, 16, 4096, 4096, 64, 3,
+                               None, 0, None) == _lib.DFMI_EINVAL
+    assert b"bits=3" in lib.dfmi_last_error()
+    assert lib.dfmi_qmm_affine(None, _lib.DFMI_BF16, None, None, None, None, 16, 4096, 4096, 48, 4,
+                               None, 0, None) == _lib.DFMI_EINVAL
+    assert lib.dfmi_qmm_affine(None, _lib.DFMI_F32, None, None, None, None, 16, 4096, 4096, 64, 4,
+                               None, 0, None) == _lib.DFMI_EINVAL
+    assert lib.dfmi_qmm_affine(None, _lib.DFMI_BF16, None, None, None, None, 16, 4100, 4096, 64, 4,
+                               None, 0, None) == _lib.DFMI_EINVAL
+    # null pointers with a valid shape
+    assert lib.dfmi_qmm_affine(None, _lib.DFMI_BF16, None, None, None, None, 16, 4096, 4096, 64, 4,
+                               None, 0, None) == _lib.DFMI_EINVAL
+    assert b"null" in lib.dfmi_last_error()
+    # empty problems are a no-op
+    assert lib.dfmi_qmm_affine(None, _lib.DFMI_BF16, None, None, None, None, 0, 4096, 4096, 64, 4,
+                               None, 0, None) == _lib.DFMI_OK
+    assert lib.dfmi_gather_qmm_affine(None, _lib.DFMI_BF16, 4, None, None, None, None, None, None,
+                                      8, 256, 64, 4, 64, 8, None) == _lib.DFMI_EINVAL
+    assert lib.dfmi_moe_combine(None, _lib.DFMI_F32, None, None, 4, 2, 8, None) == _lib.DFMI_EINVAL
+
+
+def test_workspace_queries(lib):
+    # split-K plans need a counter region plus fp32 partials; unsplit plans none
+    assert lib.dfmi_qmm_workspace_bytes(16, 4096, 4096, 64, 4) >= 0
+    big = lib.dfmi_qmm_workspace_bytes(16, 12288, 4096, 64, 4)
+    assert big == 0 or big >= 65536 + 16 * 4096 * 4 * 2
+    assert lib.dfmi_qmm_workspace_bytes(16, 4096, 4096, 64, 3) == 0
+    assert lib.dfmi_greedy_workspace_bytes(16) >= 256 + 8 * 16
+    assert lib.dfmi_lmhead_workspace_bytes(16) >= 256 + 8 * 16
