@@ -1,5 +1,5 @@
 #!/usr/bin/env python3
-"""Benchmark of the verify-path int4 qmm on one MI355X.
+"""Benchmark of the verify-path int4 matmuls on one MI355X.
 
 Default workload: the 9B-class dense verify-linear sweep -- 32 layers x
 {q 4096->4096, k 4096->1024, v 4096->1024, o 4096->4096, gate 4096->12288,
@@ -11,14 +11,18 @@ and the pass streams every byte once, so the 256 MB infinity cache cannot
 hold the working set.
 
 Prints one JSON line: value = algorithmic GB/s of the step (packed weights +
-bf16 scales/biases + x + y), plus us_per_call, the HBM roofline fraction of
-the qmm kernel and a CPU baseline (the oracle's C restatement on this host's
-cores, on a bounded sample: layer 0's seven matmuls).
+bf16 scales/biases + x + y), us_per_call, the HBM roofline of the dominant
+kernel (its launches replayed alone and timed with HIP events on the stream
+they run on; ``traffic`` = measured HBM bytes per launch from the rocprofv3
+FETCH_SIZE / WRITE_SIZE summary in profiles/, when one exists for this
+workload and kernel) and a CPU baseline (the oracle's C restatement on this
+host's cores, on a bounded sample: layer 0's seven matmuls).
 
-Other workloads (``--workload``): ``single`` ([16,4096]x[4096,4096], weights
-rotated over a 1 GB pool), ``27b`` (64 layers, hidden 5120, ``--m`` 8/16/32),
-``lmhead`` (fused lm_head [16,5120]x[151936,5120] + greedy accept) and
-``moe`` (40 layers of top-8-of-256 routed experts).
+Other workloads (``--workload``, not the default line): ``27b`` (64 layers,
+hidden 5120, ``--m`` 8/16/32), ``single`` ([16,4096]x[4096,4096], weights
+rotated over a 1 GB pool), ``lmhead`` (fused lm_head [16,5120]x[151936,5120]
++ greedy accept) and ``moe`` (40 layers of top-8-of-256 routed experts,
+hidden 2048, expert width 512).
 """
 
 from __future__ import annotations
@@ -26,6 +30,7 @@ from __future__ import annotations
 import argparse
 import ctypes
 import json
+import math
 import os
 import sys
 import time
@@ -35,6 +40,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 METRIC = "M=16 int4 verify_qmm µs/call + achieved HBM GB/s (% of peak), 1 GPU"
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 
 SHAPES_9B = [("q", 4096, 4096), ("k", 4096, 1024), ("v", 4096, 1024), ("o", 4096, 4096),
              ("gate", 4096, 12288), ("up", 4096, 12288), ("down", 12288, 4096)]
@@ -56,6 +62,35 @@ def make_weights(torch, quantize, K, N, gen, dev, gs=64):
     w_q, s, b = quantize(w, gs, 4, torch.bfloat16)
     del w
     return w_q, s, b
+
+
+def graph_of(torch, fn):
+    """Capture fn() into a HIP graph on a side stream (after one eager run)."""
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        fn()
+    stream.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def time_replays(torch, g, reps, warmup=2):
+    """ms per replay of graph g, HIP events on the stream replay() launches on."""
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    cur = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(cur)
+    for _ in range(reps):
+        g.replay()
+    e1.record(cur)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
 
 
 def cpu_baseline(torch, layer, M):
@@ -103,14 +138,48 @@ def cpu_baseline(torch, layer, M):
                       f"{el:.1f} s, oracle/cpu_qmm.c OpenMP fp32-accumulate on {cpu_model}"}
 
 
-def run_sweep(args, torch, pkg):
+def measured_traffic(workload, kernel):
+    """HBM bytes per launch from the committed rocprofv3 PMC summary, or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            entry = json.load(f).get(workload, {}).get(kernel)
+    except (OSError, ValueError):
+        return None
+    if not entry:
+        return None
+    return entry.get("bytes_per_launch")
+
+
+def base_result(args, value, ms, n_calls, config, roofline):
+    return {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "us_per_call": round(ms * 1e3 / n_calls, 3),
+        "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights quantised int4 gs64 on GPU)",
+        "config": config,
+        "roofline": roofline,
+    }
+
+
+def run_sweep(args, torch):
     from dflash_mlx_amd import _lib, _runtime
     from dflash_mlx_amd.quantize import quantize
     from dflash_mlx_amd.verify_qmm import qmm_launch
 
     dev = torch.device("cuda:0")
-    shapes = SHAPES_9B if args.workload == "9b" else SHAPES_27B
-    layers = 32 if args.workload == "9b" else 64
+    big = args.workload == "27b"
+    shapes = SHAPES_27B if big else SHAPES_9B
+    layers = 64 if big else 32
     M = args.m
     gen = torch.Generator(device=dev)
     calls = []
@@ -131,83 +200,199 @@ def run_sweep(args, torch, pkg):
     tuning = None
     if args.path or args.tiles or args.splits:
         tuning = _lib.QmmTuning(args.path, args.tiles, args.splits, args.splits)
-    # size the workspace before any capture
-    need = 0
     lib = _lib.load()
     tptr = ctypes.byref(tuning) if tuning is not None else None
-    for (x, w_q, _, _, _) in calls:
-        need = max(need, lib.dfmi_qmm_workspace_bytes_ex(M, x.shape[1], w_q.shape[0], 64, 4, tptr))
+    need = max(lib.dfmi_qmm_workspace_bytes_ex(M, x.shape[1], w.shape[0], 64, 4, tptr)
+               for (x, w, _, _, _) in calls)
 
-    def step():
-        for (x, w_q, s, b, y) in calls:
-            qmm_launch(x, w_q, s, b, w_q.shape[0], 64, 4, tuning, out=y)
+    def launches(subset):
+        def fn():
+            for (x, w_q, s, b, y) in subset:
+                qmm_launch(x, w_q, s, b, w_q.shape[0], 64, 4, tuning, out=y)
+        return fn
 
-    stream = torch.cuda.Stream()
-    with torch.cuda.stream(stream):
-        _runtime.WORKSPACES.reserve(dev, need)
-        step()
-    stream.synchronize()
-    graph = None
-    if not args.no_graph:
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=stream):
-            step()
-        torch.cuda.synchronize()
-
-    def run_once():
-        if graph is not None:
-            graph.replay()
-        else:
-            with torch.cuda.stream(stream):
+    if args.no_graph:
+        stream = torch.cuda.Stream()
+        step = launches(calls)
+        with torch.cuda.stream(stream):
+            _runtime.WORKSPACES.reserve(dev, need)
+            for _ in range(args.warmup):
                 step()
-
-    for _ in range(args.warmup):
-        run_once()
-    torch.cuda.synchronize()
-    cur = torch.cuda.current_stream() if graph is not None else stream
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t_wall = time.perf_counter()
-    ev0.record(cur)
-    for _ in range(args.steps):
-        run_once()
-    ev1.record(cur)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t_wall
-    ms = ev0.elapsed_time(ev1) / args.steps
-    log(f"timed {args.steps} steps: {ms:.3f} ms/step (events), wall {wall * 1e3 / args.steps:.3f} ms")
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        with torch.cuda.stream(stream):
+            for _ in range(args.steps):
+                step()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / args.steps
+    else:
+        g = graph_of(torch, launches(calls))
+        ms = time_replays(torch, g, args.steps, warmup=args.warmup)
+    log(f"timed {args.steps} steps: {ms:.3f} ms/step")
     gbs = step_bytes / (ms * 1e-3) / 1e9
-    n_calls = len(calls)
-    res = {
-        "metric": METRIC,
-        "value": round(gbs, 2),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms, 4),
-        "us_per_call": round(ms * 1e3 / n_calls, 3),
-        "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights quantised int4 gs64 on GPU)",
-        "config": {"workload": f"{args.workload}-class dense verify-linear sweep",
-                   "layers": layers, "linears_per_layer": len(shapes), "M": M,
-                   "group_size": 64, "bits": 4,
-                   "launch": "hip-graph" if graph is not None else "eager",
-                   "algorithmic_bytes_per_step": step_bytes},
-        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "qmm_dense_kernel",
-                     "bytes_per_launch_avg": step_bytes // n_calls,
-                     "us_per_launch_avg": round(ms * 1e3 / n_calls, 3)},
-    }
-    if not args.no_cpu:
+
+    # dominant kernel: the calls of each kernel replayed alone
+    groups = {}
+    for c in calls:
+        name = lib.dfmi_qmm_kernel_name(M, c[0].shape[1], c[1].shape[0], 64, 4, tptr).decode()
+        groups.setdefault(name, []).append(c)
+    per_kernel = {}
+    reps = max(3, args.steps // 4)
+    for name, subset in groups.items():
+        gk = graph_of(torch, launches(subset))
+        kms = time_replays(torch, gk, reps)
+        del gk
+        kbytes = sum(alg_bytes(M, x.shape[1], w.shape[0]) for (x, w, _, _, _) in subset)
+        per_kernel[name] = {"launches_per_step": len(subset), "ms_per_step": round(kms, 4),
+                            "us_per_launch": round(kms * 1e3 / len(subset), 3),
+                            "bytes_per_launch": kbytes // len(subset),
+                            "GBps": round(kbytes / (kms * 1e-3) / 1e9, 2)}
+    dom = max(per_kernel, key=lambda k: per_kernel[k]["ms_per_step"])
+    d = per_kernel[dom]
+    roofline = {"bound": "hbm", "achieved": d["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(d["GBps"] / HBM_PEAK_GBS, 4),
+                "traffic": measured_traffic(args.workload, dom),
+                "kernel": dom, "bytes_per_launch": d["bytes_per_launch"],
+                "us_per_launch": d["us_per_launch"], "per_kernel": per_kernel}
+    config = {"workload": f"{args.workload}-class dense verify-linear sweep",
+              "layers": layers, "linears_per_layer": len(shapes), "M": M, "group_size": 64,
+              "bits": 4, "launch": "eager" if args.no_graph else "hip-graph",
+              "algorithmic_bytes_per_step": step_bytes}
+    res = base_result(args, gbs, ms, len(calls), config, roofline)
+    if not args.no_cpu and args.workload == "9b":
         res["cpu_baseline"] = cpu_baseline(torch, calls[:len(shapes)], M)
     return res
+
+
+def run_single(args, torch):
+    from dflash_mlx_amd.quantize import quantize
+    from dflash_mlx_amd.verify_qmm import qmm_launch
+
+    dev = torch.device("cuda:0")
+    M, K, N = args.m, 4096, 4096
+    per = N * K // 2 + 4 * N * K // 64
+    R = max(2, math.ceil(1.0e9 / per))
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1)
+    w_q, s, b = make_weights(torch, quantize, K, N, gen, dev)
+    pool = [(w_q.clone(), s.clone(), b.clone()) for _ in range(R)]
+    del w_q, s, b
+    xg = torch.Generator(device=dev)
+    xg.manual_seed(0)
+    x = torch.randn((M, K), generator=xg, device=dev).to(torch.bfloat16)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+
+    def fn():
+        for (wq, sc, bi) in pool:
+            qmm_launch(x, wq, sc, bi, N, 64, 4, None, out=y)
+
+    g = graph_of(torch, fn)
+    ms = time_replays(torch, g, args.steps, warmup=args.warmup)
+    us = ms * 1e3 / R
+    gbs = alg_bytes(M, K, N) / (us * 1e-6) / 1e9
+    from dflash_mlx_amd import _lib
+
+    name = _lib.load().dfmi_qmm_kernel_name(M, K, N, 64, 4, None).decode()
+    roofline = {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic("single", name),
+                "kernel": name, "bytes_per_launch": alg_bytes(M, K, N), "us_per_launch": round(us, 3)}
+    config = {"workload": "single call [16,4096]x[4096,4096] int4 gs64, weights rotated over "
+                          f"{R} copies (1 GB)", "M": M, "K": K, "N": N}
+    return base_result(args, gbs, ms, R, config, roofline)
+
+
+def run_lmhead(args, torch):
+    from dflash_mlx_amd.lm_head import lm_head_greedy_accept
+    from dflash_mlx_amd.quantize import quantize
+
+    dev = torch.device("cuda:0")
+    M, K, V = 16, 5120, 151936
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(5)
+    w_q = torch.empty((V, K // 8), dtype=torch.int32, device=dev)
+    s = torch.empty((V, K // 64), dtype=torch.bfloat16, device=dev)
+    b = torch.empty_like(s)
+    for r0 in range(0, V, 16384):  # quantise in row blocks (fp32 W would be 3 GB)
+        r1 = min(V, r0 + 16384)
+        w = torch.randn((r1 - r0, K), generator=gen, device=dev) * 0.02
+        w_q[r0:r1], s[r0:r1], b[r0:r1] = quantize(w, 64, 4, torch.bfloat16)
+        del w
+    h = torch.randn((M, K), generator=gen, device=dev).to(torch.bfloat16)
+    ids = torch.randint(0, V, (M,), generator=gen, device=dev, dtype=torch.int32)
+
+    def fn():
+        lm_head_greedy_accept(h, w_q, s, b, verify_ids=ids, group_size=64)
+
+    g = graph_of(torch, fn)
+    ms = time_replays(torch, g, args.steps, warmup=args.warmup)
+    nbytes = V * K // 2 + 4 * V * K // 64 + 2 * M * K + 12 * M
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(gbs / HBM_PEAK_GBS, 4),
+                "traffic": measured_traffic("lmhead", "lmhead_greedy_kernel"),
+                "kernel": "lmhead_greedy_kernel", "bytes_per_launch": nbytes,
+                "us_per_launch": round(ms * 1e3, 3)}
+    config = {"workload": "fused lm_head [16,5120]x[151936,5120] int4 gs64 + greedy + accept",
+              "M": M, "K": K, "V": V}
+    return base_result(args, gbs, ms, 1, config, roofline)
+
+
+def run_moe(args, torch):
+    from dflash_mlx_amd.moe import gather_qmm, gather_swiglu, moe_combine
+    from dflash_mlx_amd.quantize import quantize
+
+    dev = torch.device("cuda:0")
+    T, k, E, D, I, layers = 16, 8, 256, 2048, 512, 40
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(7)
+
+    def experts(N, K):
+        wq = torch.empty((E, N, K // 8), dtype=torch.int32, device=dev)
+        sc = torch.empty((E, N, K // 64), dtype=torch.bfloat16, device=dev)
+        bi = torch.empty_like(sc)
+        for e in range(E):
+            w = torch.randn((N, K), generator=gen, device=dev) * 0.02
+            wq[e], sc[e], bi[e] = quantize(w, 64, 4, torch.bfloat16)
+        return wq, sc, bi
+
+    lay = []
+    total = 0
+    for _ in range(layers):
+        gate, up, down = experts(I, D), experts(I, D), experts(D, I)
+        logits = torch.randn((T, E), generator=gen, device=dev)
+        probs = torch.softmax(logits, dim=-1)
+        sc, inds = torch.topk(probs, k, dim=-1)
+        sc = (sc / sc.sum(-1, keepdim=True)).float()
+        flat = inds.reshape(-1)
+        order = torch.argsort(flat, stable=True)
+        rhs = flat[order].to(torch.int32)
+        lhs = (order // k).to(torch.int32)
+        inv = torch.empty_like(order)
+        inv[order] = torch.arange(order.numel(), device=dev)
+        n_e = int(torch.unique(flat).numel())
+        total += n_e * 3 * (I * D // 2 + 4 * I * D // 64) + 2 * T * D * 2
+        x = torch.randn((T, D), generator=gen, device=dev).to(torch.bfloat16)
+        lay.append((gate, up, down, rhs, lhs, inv, sc, x))
+    log(f"moe weights ready ({layers} layers)")
+
+    def fn():
+        for (gate, up, down, rhs, lhs, inv, sc, x) in lay:
+            h = gather_swiglu(x, gate, up, rhs, lhs_indices=lhs, group_size=64)
+            y = gather_qmm(h, *down, rhs, group_size=64)
+            moe_combine(y[inv], sc)
+
+    g = graph_of(torch, fn)
+    ms = time_replays(torch, g, args.steps, warmup=args.warmup)
+    gbs = total / (ms * 1e-3) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(gbs / HBM_PEAK_GBS, 4),
+                "traffic": measured_traffic("moe", "gather_kernel"), "kernel": "gather_kernel",
+                "bytes_per_launch": total // (2 * layers), "us_per_launch": None}
+    config = {"workload": "MoE 40 layers, 16 tokens top-8 of 256 experts, hidden 2048, "
+                          "expert width 512, int4 gs64", "algorithmic_bytes_per_step": total}
+    return base_result(args, gbs, ms, 3 * layers, config, roofline)
 
 
 def main():
@@ -215,7 +400,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="9b", choices=["9b", "27b"])
+    ap.add_argument("--workload", default="9b", choices=["9b", "27b", "single", "lmhead", "moe"])
     ap.add_argument("--m", type=int, default=16)
     ap.add_argument("--path", type=int, default=0, help="1 general kernel, 2 streaming kernel")
     ap.add_argument("--tiles", type=int, default=0)
@@ -224,15 +409,17 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU only (--gpus 1); the "
-                                   "multi-GPU sharding is a design note, not a run"}))
+        print(json.dumps({"error": "this build measures one GPU only (--gpus 1); how the path "
+                                   "shards over several GPUs is a design note, not a run"}))
         sys.exit(2)
     import torch
 
     import __graft_entry__
 
-    pkg = __graft_entry__.load_package()
-    res = run_sweep(args, torch, pkg)
+    __graft_entry__.load_package()
+    runner = {"9b": run_sweep, "27b": run_sweep, "single": run_single, "lmhead": run_lmhead,
+              "moe": run_moe}[args.workload]
+    res = runner(args, torch)
     print(json.dumps(res), flush=True)
 
 

@@ -46,6 +46,8 @@ _SIGNATURES = {
                                   _i64, _i64, _i64, _int, _int, _c_void_p, _size,
                                   ctypes.POINTER(QmmTuning), _c_void_p]),
     "dfmi_qmm_workspace_bytes": (_size, [_i64, _i64, _i64, _int, _int]),
+    "dfmi_qmm_kernel_name": (ctypes.c_char_p, [_i64, _i64, _i64, _int, _int,
+                                               ctypes.POINTER(QmmTuning)]),
     "dfmi_qmm_workspace_bytes_ex": (_size, [_i64, _i64, _i64, _int, _int,
                                             ctypes.POINTER(QmmTuning)]),
     "dfmi_gather_qmm_affine": (_int, [_c_void_p, _int, _i64, _c_void_p, _c_void_p, _c_void_p,

@@ -248,16 +248,39 @@ __global__ __launch_bounds__(64 * WV) void qmm_stream_kernel(StreamArgs a) {
   }
   stage_barrier<0>();
   if (!*s_last) return;
-  for (int idx = threadIdx.x; idx < a.M * S::NB; idx += kThreads) {
-    const int m = idx / S::NB, n = cx.n0 + idx % S::NB;
-    if (n < a.N) {
-      float sum = 0.f;
-      for (int q = 0; q < a.kp; ++q)
-        sum += __hip_atomic_load(a.partials + ((int64_t)q * a.M + m) * a.N + n, __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_AGENT);
-      a.y[(int64_t)m * a.N + n] = Num<Tag>::f2h(sum);
-    }
+  // Sum the kp partials of this thread's outputs in split order.  The
+  // device-coherent loads of four splits x PER outputs are issued together
+  // (one memory round trip per four splits, not one per load).
+  float sum[PER];
+  int64_t off[PER];
+  bool ok[PER];
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    sum[q] = 0.f;
+    ok[q] = mi[q] < a.M && ni[q] < a.N;
+    off[q] = ok[q] ? (int64_t)mi[q] * a.N + ni[q] : 0;
   }
+  const int64_t split = (int64_t)a.M * a.N;
+  for (int q0 = 0; q0 < a.kp; q0 += 4) {
+    // unconditional loads (a split past kp re-reads the last one and is
+    // dropped), so the block is straight-line code with one wait
+    float t[4][PER];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t base = (int64_t)min(q0 + j, a.kp - 1) * split;
+#pragma unroll
+      for (int q = 0; q < PER; ++q)
+        t[j][q] = __hip_atomic_load(a.partials + base + off[q], __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int q = 0; q < PER; ++q) sum[q] += (q0 + j < a.kp) ? t[j][q] : 0.f;
+  }
+#pragma unroll
+  for (int q = 0; q < PER; ++q)
+    if (ok[q]) a.y[(int64_t)mi[q] * a.N + ni[q]] = Num<Tag>::f2h(sum[q]);
   if (threadIdx.x == 0)
     __hip_atomic_exchange(&a.counters[nb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -298,6 +321,9 @@ static int plan_stream(int64_t M, int64_t K, int64_t N, int gs, const dfmi_qmm_t
   p.kp = std::max(1, std::min(kp, (int)(K / 256)));
   if (p.n_blocks > kMaxCounters) p.kp = 1;
   p.WV = stream_waves(M, K, p.n_blocks * p.kp);
+  if (tune && (tune->waves_per_block == 4 || tune->waves_per_block == 8) &&
+      (tune->waves_per_block == 4 || (M <= 16 && K % 512 == 0)))
+    p.WV = tune->waves_per_block;
   p.chunks = (int)(K / (64 * p.WV));
   p.kp = std::min(p.kp, p.chunks);
   p.xcd_map = (p.n_blocks % 8 == 0) ? 1 : 0;
@@ -388,14 +414,13 @@ static int validate_qmm(int x_dtype, int64_t M, int64_t K, int64_t N, int gs, in
 
 using namespace dfmi;
 
-// Automatic choice (measured on MI355X): the streaming kernel wins once a
-// call has enough weight rows (N >= 8192) or a long enough K (>= 8192) to
-// keep its pipeline full; smaller calls go to the general kernel.
+// Automatic choice (measured on MI355X): the streaming kernel is faster on
+// every shape it takes; the general kernel covers the rest (M > 32, K not a
+// multiple of 256 or of 8 groups, weights over 2 GiB).
 static bool use_stream(int64_t M, int64_t K, int64_t N, int gs, const dfmi_qmm_tuning* tune) {
   const int path = tune ? tune->path : 0;
-  if (path == 1 || !stream_eligible(M, K, N, gs)) return false;
-  if (path == 2) return true;
-  return N >= 8192 || K >= 8192;
+  if (path == 1) return false;
+  return stream_eligible(M, K, N, gs);
 }
 
 extern "C" size_t dfmi_qmm_workspace_bytes_ex(int64_t M, int64_t K, int64_t N, int group_size,
@@ -405,6 +430,12 @@ extern "C" size_t dfmi_qmm_workspace_bytes_ex(int64_t M, int64_t K, int64_t N, i
   StreamPlan p;
   if (plan_stream(M, K, N, group_size, tuning, p) != DFMI_OK) return 0;
   return p.ws_bytes;
+}
+
+extern "C" const char* dfmi_qmm_kernel_name(int64_t M, int64_t K, int64_t N, int group_size,
+                                             int bits, const dfmi_qmm_tuning* tuning) {
+  if (validate_qmm(DFMI_BF16, M, K, N, group_size, bits) != DFMI_OK) return nullptr;
+  return use_stream(M, K, N, group_size, tuning) ? "qmm_stream_kernel" : "qmm_dense_kernel";
 }
 
 extern "C" size_t dfmi_qmm_workspace_bytes(int64_t M, int64_t K, int64_t N, int group_size,

@@ -53,7 +53,8 @@ const char *dfmi_last_error(void);
  *   tiles_per_wave: general kernel, 16-row weight tiles per wavefront (1, 2,
  *         4; the streaming kernel always covers 64 rows per workgroup);
  *   waves_per_block: general kernel, wavefronts of a workgroup that split K
- *         (1..8; the reference's K_PARTS);
+ *         (1..8; the reference's K_PARTS); streaming kernel, 4 or 8
+ *         wavefronts (8 needs M <= 16 and K % 512 == 0);
  *   k_splits: streaming kernel, workgroups that split K of one output block. */
 typedef struct dfmi_qmm_tuning {
   int path;
@@ -91,6 +92,11 @@ int dfmi_qmm_affine_ex(const void *x, int x_dtype, const uint32_t *w_q, const vo
                        int group_size, int bits, void *workspace, size_t workspace_bytes,
                        const dfmi_qmm_tuning *tuning, void *stream);
 size_t dfmi_qmm_workspace_bytes(int64_t M, int64_t K, int64_t N, int group_size, int bits);
+/* Host-only plan query (no reference counterpart; for benchmarks and
+ * profiles): name of the kernel dfmi_qmm_affine_ex would launch for this
+ * shape, "qmm_stream_kernel" or "qmm_dense_kernel"; NULL if unsupported. */
+const char *dfmi_qmm_kernel_name(int64_t M, int64_t K, int64_t N, int group_size, int bits,
+                                 const dfmi_qmm_tuning *tuning);
 size_t dfmi_qmm_workspace_bytes_ex(int64_t M, int64_t K, int64_t N, int group_size, int bits,
                                    const dfmi_qmm_tuning *tuning);
 
