@@ -22,7 +22,8 @@ Other workloads (``--workload``, not the default line): ``27b`` (64 layers,
 hidden 5120, ``--m`` 8/16/32), ``single`` ([16,4096]x[4096,4096], weights
 rotated over a 1 GB pool), ``lmhead`` (fused lm_head [16,5120]x[151936,5120]
 + greedy accept) and ``moe`` (40 layers of top-8-of-256 routed experts,
-hidden 2048, expert width 512).
+hidden 2048, expert width 512).  ``copy`` is a 512 MiB device copy used to
+calibrate the HBM traffic counters.
 """
 
 from __future__ import annotations
@@ -395,12 +396,36 @@ def run_moe(args, torch):
     return base_result(args, gbs, ms, 3 * layers, config, roofline)
 
 
+def run_copy(args, torch):
+    """Plain device copy of a known size: calibrates the FETCH_SIZE /
+    WRITE_SIZE counters (bytes per dispatch read and written are both
+    exactly 512 MiB)."""
+    dev = torch.device("cuda:0")
+    n = 512 * 1024 * 1024 // 4
+    src = torch.ones(n, dtype=torch.int32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(args.warmup):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    gbs = 2 * n * 4 / (ms * 1e-3) / 1e9
+    return {"workload": "copy 512 MiB (counter calibration)", "bytes_read": n * 4,
+            "bytes_written": n * 4, "ms_per_copy": round(ms, 4), "GBps_read_plus_write": round(gbs, 1)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="9b", choices=["9b", "27b", "single", "lmhead", "moe"])
+    ap.add_argument("--workload", default="9b",
+                    choices=["9b", "27b", "single", "lmhead", "moe", "copy"])
     ap.add_argument("--m", type=int, default=16)
     ap.add_argument("--path", type=int, default=0, help="1 general kernel, 2 streaming kernel")
     ap.add_argument("--tiles", type=int, default=0)
@@ -418,7 +443,7 @@ def main():
 
     __graft_entry__.load_package()
     runner = {"9b": run_sweep, "27b": run_sweep, "single": run_single, "lmhead": run_lmhead,
-              "moe": run_moe}[args.workload]
+              "moe": run_moe, "copy": run_copy}[args.workload]
     res = runner(args, torch)
     print(json.dumps(res), flush=True)
 
