@@ -28,3 +28,9 @@ inline int check_launch(const char* what) {
 inline size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 }  // namespace dfmi
+
+// 8-bit affine qmm launch (dfmi_qmm8.hip), called by dfmi_qmm_affine_ex after
+// its argument checks.
+int dfmi_qmm8_launch(const void* x, int x_dtype, const uint32_t* w_q, const void* scales,
+                     const void* biases, void* y, int64_t M, int64_t K, int64_t N, int gs,
+                     void* stream);

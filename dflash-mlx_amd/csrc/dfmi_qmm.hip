@@ -388,8 +388,8 @@ static int validate_qmm(int x_dtype, int64_t M, int64_t K, int64_t N, int gs, in
     set_error("dfmi_qmm: x dtype %d unsupported (bf16 or f16)", x_dtype);
     return DFMI_EINVAL;
   }
-  if (bits != 4) {
-    set_error("dfmi_qmm: bits=%d unsupported (4)", bits);
+  if (bits != 4 && bits != 8) {
+    set_error("dfmi_qmm: bits=%d unsupported (4 or 8)", bits);
     return DFMI_EINVAL;
   }
   if (gs != 32 && gs != 64 && gs != 128) {
@@ -402,7 +402,7 @@ static int validate_qmm(int x_dtype, int64_t M, int64_t K, int64_t N, int gs, in
     return DFMI_EINVAL;
   }
   if (M >= (1ll << 31) || N >= (1ll << 31) || K >= (1ll << 31) ||
-      N * (K / 8) > 0xFFFFFFFFll) {
+      N * (K * bits / 32) > 0xFFFFFFFFll) {
     set_error("dfmi_qmm: shape too large M=%lld K=%lld N=%lld", (long long)M, (long long)K,
               (long long)N);
     return DFMI_EINVAL;
@@ -417,16 +417,20 @@ using namespace dfmi;
 // Automatic choice (measured on MI355X): the streaming kernel is faster on
 // every shape it takes; the general kernel covers the rest (M > 32, K not a
 // multiple of 256 or of 8 groups, weights over 2 GiB).
-static bool use_stream(int64_t M, int64_t K, int64_t N, int gs, const dfmi_qmm_tuning* tune) {
+static bool use_stream(int64_t M, int64_t K, int64_t N, int gs, int bits,
+                       const dfmi_qmm_tuning* tune) {
   const int path = tune ? tune->path : 0;
+  if (bits != 4) return false;
   if (path == 1) return false;
   return stream_eligible(M, K, N, gs);
 }
 
 extern "C" size_t dfmi_qmm_workspace_bytes_ex(int64_t M, int64_t K, int64_t N, int group_size,
                                               int bits, const dfmi_qmm_tuning* tuning) {
-  if (validate_qmm(DFMI_BF16, M, K, N, group_size, bits) != DFMI_OK || M == 0 || N == 0) return 0;
-  if (!use_stream(M, K, N, group_size, tuning)) return 0;
+  if (validate_qmm(DFMI_BF16, M, K, N, group_size, bits) != DFMI_OK || M == 0 || N == 0 ||
+      bits != 4)
+    return 0;
+  if (!use_stream(M, K, N, group_size, bits, tuning)) return 0;
   StreamPlan p;
   if (plan_stream(M, K, N, group_size, tuning, p) != DFMI_OK) return 0;
   return p.ws_bytes;
@@ -435,7 +439,8 @@ extern "C" size_t dfmi_qmm_workspace_bytes_ex(int64_t M, int64_t K, int64_t N, i
 extern "C" const char* dfmi_qmm_kernel_name(int64_t M, int64_t K, int64_t N, int group_size,
                                              int bits, const dfmi_qmm_tuning* tuning) {
   if (validate_qmm(DFMI_BF16, M, K, N, group_size, bits) != DFMI_OK) return nullptr;
-  return use_stream(M, K, N, group_size, tuning) ? "qmm_stream_kernel" : "qmm_dense_kernel";
+  if (bits == 8) return "qmm8_kernel";
+  return use_stream(M, K, N, group_size, bits, tuning) ? "qmm_stream_kernel" : "qmm_dense_kernel";
 }
 
 extern "C" size_t dfmi_qmm_workspace_bytes(int64_t M, int64_t K, int64_t N, int group_size,
@@ -460,12 +465,14 @@ extern "C" int dfmi_qmm_affine_ex(const void* x, int x_dtype, const uint32_t* w_
     return DFMI_EINVAL;
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (bits == 8) return dfmi_qmm8_launch(x, x_dtype, w_q, scales, biases, y, M, K, N, group_size,
+                                         stream);
   if (tuning && tuning->path == 2 && !stream_eligible(M, K, N, group_size)) {
     set_error("dfmi_qmm: shape M=%lld K=%lld gs=%d outside the streaming kernel", (long long)M,
               (long long)K, group_size);
     return DFMI_EINVAL;
   }
-  if (use_stream(M, K, N, group_size, tuning)) {
+  if (use_stream(M, K, N, group_size, bits, tuning)) {
     StreamPlan p;
     rc = plan_stream(M, K, N, group_size, tuning, p);
     if (rc != DFMI_OK) return rc;

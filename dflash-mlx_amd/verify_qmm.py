@@ -131,7 +131,8 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
     ``mx.quantized_matmul`` plays for the reference): ``x . dequant(w)^T``.
 
     Raises :class:`_lib.DfmiUnsupported` for what the kernels do not cover
-    (transpose=False, bits != 4, non-affine modes, fp32 activations).
+    (transpose=False, bits other than 4 and 8, non-affine modes, fp32
+    activations).
     """
     if not transpose or mode != "affine":
         raise _lib.DfmiUnsupported(_lib.DFMI_EINVAL,

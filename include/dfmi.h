@@ -75,9 +75,11 @@ typedef struct dfmi_qmm_tuning {
  *   mx.quantized_matmul(x, w, scales, biases, transpose=True, group_size, bits)
  *     (verify_qmm.py:915-919 and every fallback site)
  * x, scales, biases: dtype x_dtype (DFMI_BF16 or DFMI_F16); y: same dtype.
- * Supported: bits == 4, group_size in {32, 64, 128}, K % 32 == 0,
- * K % group_size == 0, any M >= 1, any N >= 1; 16-byte aligned x / w_q /
- * scales / biases.  fp32 accumulation, output rounded to nearest even.
+ * Supported: bits 4 or 8 (8-bit: w_q [N, K/4], byte i of word j = k 4j+i,
+ * the reference's mma2big_8bit layout, verify_qmm.py:549-650, 767-884),
+ * group_size in {32, 64, 128}, K % 32 == 0, K % group_size == 0, any M >= 1,
+ * any N >= 1; 16-byte aligned x / w_q / scales / biases.  fp32 accumulation,
+ * output rounded to nearest even.
  * Anything else returns DFMI_EINVAL without launching.  Results do not depend
  * on scheduling: every K split is summed in a fixed order.  Shapes that split
  * K across workgroups need the workspace dfmi_qmm_workspace_bytes reports
@@ -94,7 +96,8 @@ int dfmi_qmm_affine_ex(const void *x, int x_dtype, const uint32_t *w_q, const vo
 size_t dfmi_qmm_workspace_bytes(int64_t M, int64_t K, int64_t N, int group_size, int bits);
 /* Host-only plan query (no reference counterpart; for benchmarks and
  * profiles): name of the kernel dfmi_qmm_affine_ex would launch for this
- * shape, "qmm_stream_kernel" or "qmm_dense_kernel"; NULL if unsupported. */
+ * shape, "qmm_stream_kernel", "qmm_dense_kernel" or (bits 8) "qmm8_kernel";
+ * NULL if unsupported. */
 const char *dfmi_qmm_kernel_name(int64_t M, int64_t K, int64_t N, int group_size, int bits,
                                  const dfmi_qmm_tuning *tuning);
 size_t dfmi_qmm_workspace_bytes_ex(int64_t M, int64_t K, int64_t N, int group_size, int bits,

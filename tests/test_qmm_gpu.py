@@ -21,7 +21,8 @@ GOLD = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "referen
 REL_TOL = 1e-2
 
 
-def _run(dev, x, w_q, s, b, gs, dtype="bf16", tuning=None, via="stock", monkeypatch=None):
+def _run(dev, x, w_q, s, b, gs, dtype="bf16", tuning=None, via="stock", monkeypatch=None,
+         bits=4):
     import torch
 
     from dflash_mlx_amd import verify_qmm as vq
@@ -29,9 +30,9 @@ def _run(dev, x, w_q, s, b, gs, dtype="bf16", tuning=None, via="stock", monkeypa
     xt, st, bt = to_dev(x, dtype, dev), to_dev(s, dtype, dev), to_dev(b, dtype, dev)
     wt = to_dev(w_q, "u32", dev)
     if via == "verify":
-        y = vq.verify_matmul(xt, wt, st, bt, transpose=True, group_size=gs, bits=4)
+        y = vq.verify_matmul(xt, wt, st, bt, transpose=True, group_size=gs, bits=bits)
     else:
-        y = vq.quantized_matmul(xt, wt, st, bt, transpose=True, group_size=gs, bits=4,
+        y = vq.quantized_matmul(xt, wt, st, bt, transpose=True, group_size=gs, bits=bits,
                                 tuning=tuning)
     torch.cuda.synchronize()
     return from_dev(y, dtype)
@@ -177,3 +178,33 @@ def test_unsupported_raises(dev):
     xf = torch.zeros((16, 64), dtype=torch.float32, device=dev)
     with pytest.raises(_lib.DfmiUnsupported):
         vq.quantized_matmul(xf, w[:, :8], s[:, :1], s[:, :1], group_size=64, bits=4)
+
+
+@pytest.mark.parametrize("M,K,N,gs", [(16, 4096, 1024, 64), (4, 512, 96, 32), (16, 1024, 2048, 128),
+                                      (33, 256, 40, 64), (1, 96, 16, 32)])
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_8bit_matches_oracle(dev, M, K, N, gs, dtype):
+    """bits=8 (the reference's mma2big_8bit layout, verify_qmm.py:593-598)."""
+    x, w_q, s, b = make_qmm_case(M, K, N, gs, dtype=dtype, seed=M + K + N, bits=8)
+    got = _run(dev, x, w_q, s, b, gs, dtype=dtype, bits=8)
+    want = oracle.quantized_matmul(x, w_q, s, b, group_size=gs, bits=8, dtype=dtype)
+    _, rel = oracle.parity_metrics(oracle.to_f32(got, dtype), want)
+    assert rel <= 1e-2, rel
+
+
+def test_8bit_closed_form_exact(dev):
+    """Integer activations, unit scales, small integer biases: the fp32 result is
+    exact, so the 8-bit path must be bit-exact after rounding."""
+    import torch
+
+    rng = np.random.default_rng(8)
+    M, K, N, gs = 16, 256, 64, 64
+    q = rng.integers(0, 256, size=(N, K))
+    w_q = oracle.pack(q, 8)
+    s = oracle.round_to_dtype(np.ones((N, K // gs), np.float32), "bf16")
+    b = oracle.round_to_dtype(rng.integers(-2, 3, size=(N, K // gs)).astype(np.float32), "bf16")
+    x = oracle.round_to_dtype(rng.integers(-2, 3, size=(M, K)).astype(np.float32), "bf16")
+    want = oracle.quantized_matmul(x, w_q, s, b, group_size=gs, bits=8, dtype="bf16",
+                                   out_dtype="bf16")
+    got = _run(dev, x, w_q, s, b, gs, bits=8)
+    assert np.array_equal(got, want)
