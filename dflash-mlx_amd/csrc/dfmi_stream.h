@@ -8,8 +8,8 @@
 //     every few cycles however few bytes of the line an instruction uses, so
 //     every global read is a whole-line request: weights (whole 32*WV-byte
 //     row pieces), activations (whole rows) and scales / biases (8 rows x
-//     64 B of each array) go straight to LDS with global_load_lds_dwordx4,
-//     kDepth steps ahead;
+//     64 B of each array) go straight to LDS with buffer_load ... lds,
+//     DEPTH - 1 steps ahead;
 //   * the loop is VALU-issue bound (a SIMD retires one wave64 VALU op per
 //     ~4.2 cycles), so every address is computed once per lane: a DMA is an
 //     SGPR base (advanced by scalar adds) plus a lane-constant VGPR offset,
@@ -47,7 +47,6 @@ namespace dfmi {
 
 constexpr int kStreamRows = 64;   // weight rows per workgroup
 constexpr int kStreamTiles = 4;   // 16-row MFMA tiles per workgroup, all in every wavefront
-constexpr int kDepth = 3;         // LDS stages
 
 // Wait until at most N vector-memory operations of this wavefront are
 // outstanding and all LDS operations are done, then the workgroup barrier.
@@ -107,6 +106,14 @@ struct Stream {
   static constexpr int WPPR = WROW / 16;    // 16-byte pieces per weight row
   static_assert(WV == 4 || WV == 8, "wavefronts");
   static_assert(SBC >= 2, "scale block reuse distance");
+  // LDS stages (DEPTH - 1 steps in flight).  A scale block's buffer is
+  // rewritten DEPTH - 1 steps ahead of its last reader, so SBC >= DEPTH - 1
+  // keeps the two scale buffers apart.  Four stages with 8 wavefronts
+  // (144 KB of LDS) measured slower than three on MI355X (4096x12288:
+  // 12.8 us vs 11.4 us): the extra step in flight does not raise the per-CU
+  // request rate, and the longer wait chain delays the first MFMA.
+  static constexpr int DEPTH = 3;
+  static_assert(SBC >= DEPTH - 1, "scale buffers");
   // gs >= 64: a lane's two k-blocks take adjacent words (one 8-byte LDS read);
   // gs = 32: k-block j is group 2*wave + j, so the blocks stay group-pure.
   static constexpr bool PAIR = GS >= 64;
@@ -117,8 +124,9 @@ struct Stream {
   // (the ds_read offset field is 16 bits).
   static constexpr int SB_OFF = 0;
   static constexpr int X_OFF = 2 * SBBUF;
-  static constexpr int W_OFF = X_OFF + kDepth * XBUF;
-  static constexpr int LDS_BYTES = W_OFF + kDepth * WBUF;
+  static constexpr int W_OFF = X_OFF + DEPTH * XBUF;
+  static constexpr int LDS_BYTES = W_OFF + DEPTH * WBUF;
+  static_assert(LDS_BYTES <= 160 * 1024, "LDS");
   // epilogue: [wave][t][mt][reg][lane] floats, aliasing the stages
   static constexpr int RED_FLOATS = NT * MT * 4 * 64;
   static_assert(WV * RED_FLOATS * 4 <= LDS_BYTES, "reduction buffer");
@@ -336,21 +344,28 @@ struct Stream {
     }
   }
 
-  // iteration c: step c+1 must be in LDS; step c is in `cur`.  The wait asks
-  // for at most CHUNK_DMA newer loads (step c+2's activations and weights):
-  // when step c+2 also brought a scale block (issued before them) this
-  // over-waits by that block, which lands with them anyway.
+  // Barrier once this wavefront has at most n whole steps of loads
+  // outstanding (n <= 3).  A scale block issued with one of those steps (it
+  // precedes their activations and weights) is over-waited: it lands with them.
+  __device__ static inline void wait_steps(int n) {
+    if (n >= 3) stage_barrier<3 * CHUNK_DMA>();
+    else if (n == 2) stage_barrier<2 * CHUNK_DMA>();
+    else if (n == 1) stage_barrier<CHUNK_DMA>();
+    else stage_barrier<0>();
+  }
+
+  // iteration c: step c+1 must be in LDS (steps c+2 .. c+DEPTH-1 may still
+  // be in flight); step c is in `cur`.
   __device__ static inline void step(const Ctx& cx, const Lane& L, int c, int c1, int stage,
                                      Frag& cur, Frag& nxt, f32x4 (&acc)[NT][MT],
                                      const DqConst& dq) {
     if (c + 1 < c1) {
-      if (c + 2 < c1) stage_barrier<CHUNK_DMA>();
-      else stage_barrier<0>();
-      if (c + 3 < c1) {
-        if ((c + 3) % SBC == 0) issue_sb(cx, (c + 3) / SBC, ((c + 3) / SBC) & 1);
-        issue_chunk(cx, L, c + 3, stage);  // step c's stage: its fragments are in cur
+      wait_steps(min(DEPTH - 2, c1 - c - 2));
+      if (c + DEPTH < c1) {
+        if ((c + DEPTH) % SBC == 0) issue_sb(cx, (c + DEPTH) / SBC, ((c + DEPTH) / SBC) & 1);
+        issue_chunk(cx, L, c + DEPTH, stage);  // step c's stage: its fragments are in cur
       }
-      const int st1 = stage == 2 ? 0 : stage + 1;
+      const int st1 = stage == DEPTH - 1 ? 0 : stage + 1;
       read_frag(cx, L, c + 1, st1, ((c + 1) / SBC) & 1, nxt);
     }
     compute(L, cur, acc, dq);
@@ -365,25 +380,22 @@ struct Stream {
     issue_sb(cx, c0 / SBC, (c0 / SBC) & 1);
     issue_chunk(cx, L, c0, 0);
 #pragma unroll
-    for (int k = 1; k < kDepth; ++k) {
+    for (int k = 1; k < DEPTH; ++k) {
       if (c0 + k < c1) {
         if ((c0 + k) % SBC == 0) issue_sb(cx, (c0 + k) / SBC, ((c0 + k) / SBC) & 1);
         issue_chunk(cx, L, c0 + k, k);
       }
     }
-    // step c0 in LDS: at most the loads of steps c0+1, c0+2 outstanding
-    // (over-waits by a scale block issued with one of them)
-    if (c0 + 2 < c1) stage_barrier<2 * CHUNK_DMA>();
-    else if (c0 + 1 < c1) stage_barrier<CHUNK_DMA>();
-    else stage_barrier<0>();
+    // step c0 in LDS: at most the loads of steps c0+1 .. c0+DEPTH-1 outstanding
+    wait_steps(min(DEPTH - 1, c1 - c0 - 1));
     Frag fa, fb;
     read_frag(cx, L, c0, 0, (c0 / SBC) & 1, fa);
     int c = c0, stage = 0;
     for (; c + 1 < c1; c += 2) {
       step(cx, L, c, c1, stage, fa, fb, acc, dq);
-      stage = stage == 2 ? 0 : stage + 1;
+      stage = stage == DEPTH - 1 ? 0 : stage + 1;
       step(cx, L, c + 1, c1, stage, fb, fa, acc, dq);
-      stage = stage == 2 ? 0 : stage + 1;
+      stage = stage == DEPTH - 1 ? 0 : stage + 1;
     }
     if (c < c1) step(cx, L, c, c1, stage, fa, fb, acc, dq);
   }
