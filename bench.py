@@ -332,8 +332,8 @@ def run_lmhead(args, torch):
     gbs = nbytes / (ms * 1e-3) / 1e9
     roofline = {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(gbs / HBM_PEAK_GBS, 4),
-                "traffic": measured_traffic("lmhead", "lmhead_greedy_kernel"),
-                "kernel": "lmhead_greedy_kernel", "bytes_per_launch": nbytes,
+                "traffic": measured_traffic("lmhead", "lmhead_stream_kernel"),
+                "kernel": "lmhead_stream_kernel", "bytes_per_launch": nbytes,
                 "us_per_launch": round(ms * 1e3, 3)}
     config = {"workload": "fused lm_head [16,5120]x[151936,5120] int4 gs64 + greedy + accept",
               "M": M, "K": K, "V": V}

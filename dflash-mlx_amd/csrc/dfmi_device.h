@@ -116,6 +116,14 @@ __device__ inline f32x4 mma_f32_16x16x4(float a, float b, f32x4 c) {
 
 __device__ inline f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
 
+// Raw buffer resource over [base, base + bytes): word 3 = 0x00020000 (32-bit
+// data format, the gfx9 raw-buffer setting); reads at or past `bytes` return
+// zero instead of touching memory.
+__device__ inline __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+
 // Monotone map float -> uint32 (larger float -> larger key); NaN maps to 0 so
 // it never wins an argmax unless every candidate is NaN.
 __device__ inline uint32_t ordered_key(float v) {

@@ -1,12 +1,14 @@
 // Greedy verify on gfx950: argmax over the vocabulary per verify row, accept
 // length against the drafted block, bonus token.
 //
-//  * lmhead_greedy_kernel: the lm_head matmul (same main loop as the dense
-//    qmm: 16*NT vocabulary rows per workgroup, K split over its wavefronts)
-//    whose epilogue rounds each logit to the activation dtype (the dtype the
+//  * lmhead_stream_kernel: the lm_head matmul on the streaming main loop (64
+//    vocabulary rows per workgroup, the whole K, LDS-DMA staging) whose
+//    epilogue rounds each logit to the activation dtype (the dtype the
 //    reference's logits carry), applies the optional Gemma softcap and the
 //    suppress mask, and reduces to a per-row (value, index) argmax key.  The
 //    logits never reach HBM unless the caller asks for them.
+//  * lmhead_greedy_kernel: the same on the general main loop, for shapes the
+//    streaming loop does not take (K not a multiple of 256 or of 8 groups).
 //  * greedy_kernel: the same reduction over logits already in memory.
 //
 // Cross-workgroup reduction: a 64-bit key (monotone value bits << 32 |
@@ -23,6 +25,7 @@
 
 #include "dfmi_core.h"
 #include "dfmi_host.h"
+#include "dfmi_stream.h"
 
 namespace dfmi {
 
@@ -117,6 +120,7 @@ struct LmArgs {
 };
 
 constexpr int kLmTiles = 4;  // 64 vocabulary rows per workgroup
+static_assert(16 * kLmTiles == kStreamRows, "one block numbering for both lm_head kernels");
 
 template <typename Tag, int GS, int MT, bool KFULL>
 __global__ __launch_bounds__(kMaxWaves * 64) void lmhead_greedy_kernel(LmArgs a) {
@@ -167,6 +171,66 @@ __global__ __launch_bounds__(kMaxWaves * 64) void lmhead_greedy_kernel(LmArgs a)
       atomicMax(&s_best[m], argmax_key(v, (uint32_t)n));
     }
   });
+  __syncthreads();
+  greedy_publish_and_finish(a.out, s_best, 0, a.M, (unsigned)a.n_blocks);
+}
+
+template <typename Tag, int GS, int MT, int WV>
+__global__ __launch_bounds__(64 * WV) void lmhead_stream_kernel(LmArgs a) {
+  using S = Stream<Tag, GS, MT, WV>;
+  constexpr int kThreads = 64 * WV;
+  __shared__ unsigned long long s_best[16 * MT];
+  const int tid = threadIdx.x;
+  if (tid < 16 * MT) s_best[tid] = 0ull;
+  typename S::Ctx cx;
+  cx.x = buffer_rsrc(a.h, (uint32_t)a.M * (uint32_t)a.K * 2u);
+  cx.w = buffer_rsrc(a.w, (uint32_t)a.V * (uint32_t)(a.K / 2));
+  cx.s = buffer_rsrc(a.s, (uint32_t)a.V * (uint32_t)(a.K / GS) * 2u);
+  cx.b = buffer_rsrc(a.b, (uint32_t)a.V * (uint32_t)(a.K / GS) * 2u);
+  cx.K = a.K;
+  cx.M = a.M;
+  cx.N = a.V;
+  cx.groups = a.K / GS;
+  cx.n0 = blockIdx.x * S::NB;
+  cx.lane = tid & 63;
+  cx.wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  f32x4 acc[S::NT][MT];
+#pragma unroll
+  for (int t = 0; t < S::NT; ++t)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[t][mt] = zero4();
+  S::run(cx, 0, a.K / S::CK, acc);
+
+  // sum the WV wavefronts' partial tiles through LDS (the stages are free:
+  // every DMA has landed and every wavefront is past its last LDS read)
+  __syncthreads();
+  float* red = reinterpret_cast<float*>(dfmi_smem);
+  {
+    float* mine = red + cx.wave * S::RED_FLOATS;
+#pragma unroll
+    for (int t = 0; t < S::NT; ++t)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) mine[((t * MT + mt) * 4 + j) * 64 + cx.lane] = acc[t][mt][j];
+  }
+  __syncthreads();
+  const float capr = a.softcap > 0.f ? round_t<Tag>(a.softcap) : 0.f;
+  const float neg = round_t<Tag>(-1e9f);
+  for (int e = tid; e < S::RED_FLOATS; e += kThreads) {
+    float sum = red[e];
+#pragma unroll
+    for (int wv = 1; wv < WV; ++wv) sum += red[wv * S::RED_FLOATS + e];
+    const int l = e & 63, j = (e >> 6) & 3, tm = e >> 8;
+    const int n = cx.n0 + (tm / MT) * 16 + (l & 15);
+    const int m = (tm % MT) * 16 + 4 * (l >> 4) + j;
+    if (m < a.M && n < a.V) {
+      float v = logit_value<Tag>(sum, capr);
+      if (a.logits) a.logits[(int64_t)m * a.V + n] = Num<Tag>::f2h(v);
+      if (a.mask && a.mask[n]) v = neg;
+      atomicMax(&s_best[m], argmax_key(v, (uint32_t)n));
+    }
+  }
   __syncthreads();
   greedy_publish_and_finish(a.out, s_best, 0, a.M, (unsigned)a.n_blocks);
 }
@@ -264,6 +328,34 @@ static void launch_lm_tag(int gs, int mt, bool kfull, int blocks, int waves, hip
   }
 }
 
+template <typename Tag, int GS, int MT, int WV>
+static void launch_lm_stream_t(int blocks, hipStream_t st, const LmArgs& a) {
+  constexpr int lds = Stream<Tag, GS, MT, WV>::LDS_BYTES;
+  // dynamic LDS above 64 KiB needs the kernel attribute raised (once)
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(&lmhead_stream_kernel<Tag, GS, MT, WV>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  (void)attr;
+  hipLaunchKernelGGL((lmhead_stream_kernel<Tag, GS, MT, WV>), dim3(blocks), dim3(64 * WV), lds,
+                     st, a);
+}
+
+// 4 wavefronts (two workgroups per CU): the vocabulary gives thousands of
+// workgroups, so the whole K stays in one workgroup (no split epilogue).
+template <typename Tag>
+static void launch_lm_stream(int gs, int mt, int blocks, hipStream_t st, const LmArgs& a) {
+  if (gs == 32) {
+    if (mt == 1) launch_lm_stream_t<Tag, 32, 1, 4>(blocks, st, a);
+    else launch_lm_stream_t<Tag, 32, 2, 4>(blocks, st, a);
+  } else if (gs == 64) {
+    if (mt == 1) launch_lm_stream_t<Tag, 64, 1, 4>(blocks, st, a);
+    else launch_lm_stream_t<Tag, 64, 2, 4>(blocks, st, a);
+  } else {
+    if (mt == 1) launch_lm_stream_t<Tag, 128, 1, 4>(blocks, st, a);
+    else launch_lm_stream_t<Tag, 128, 2, 4>(blocks, st, a);
+  }
+}
+
 }  // namespace dfmi
 
 using namespace dfmi;
@@ -346,12 +438,17 @@ extern "C" int dfmi_lmhead_greedy_accept(const void* h, int h_dtype, const uint3
   a.K = (int)K;
   a.V = (int)V;
   a.chunks = (int)((K + kChunkK - 1) / kChunkK);
-  const int nb_cols = 16 * kLmTiles;
+  const int nb_cols = 16 * kLmTiles;  // = kStreamRows
   a.n_blocks = (int)((V + nb_cols - 1) / nb_cols);
   const bool kfull = (K % kChunkK) == 0;
   const int mt = M <= 16 ? 1 : 2;
-  const int waves = a.chunks < kMaxWaves ? a.chunks : kMaxWaves;
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (stream_eligible(M, K, V, group_size)) {
+    if (h_dtype == DFMI_BF16) launch_lm_stream<BF16>(group_size, mt, a.n_blocks, st, a);
+    else launch_lm_stream<F16>(group_size, mt, a.n_blocks, st, a);
+    return check_launch("dfmi_lmhead_greedy_accept");
+  }
+  const int waves = a.chunks < kMaxWaves ? a.chunks : kMaxWaves;
   if (h_dtype == DFMI_BF16) launch_lm_tag<BF16>(group_size, mt, kfull, a.n_blocks, waves, st, a);
   else launch_lm_tag<F16>(group_size, mt, kfull, a.n_blocks, waves, st, a);
   return check_launch("dfmi_lmhead_greedy_accept");

@@ -67,14 +67,6 @@ __device__ inline void stage_barrier() {
 // Dynamic LDS of the streaming kernels (one allocation per workgroup).
 extern __shared__ __attribute__((aligned(16))) char dfmi_smem[];
 
-// Raw buffer resource over [base, base + bytes): word 3 = 0x00020000 (32-bit
-// data format, the gfx9 raw-buffer setting); reads at or past `bytes` return
-// zero instead of touching memory.
-__device__ inline __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
-                                           0x00020000);
-}
-
 // 16 bytes per lane from a buffer (lane-constant VGPR offset + wave-uniform
 // SGPR offset: no vector arithmetic per load) to LDS (wave-uniform
 // destination; lane l lands at dst + 16 l).

@@ -108,7 +108,9 @@ def _lm_case(M, K, V, gs, seed, dtype="bf16"):
 
 @pytest.mark.parametrize("M,K,V,gs,dtype", [(16, 512, 1000, 64, "bf16"), (16, 2048, 32000, 64, "bf16"),
                                             (4, 1024, 5003, 32, "f16"), (32, 768, 2048, 128, "bf16"),
-                                            (1, 256, 129, 64, "bf16"), (16, 1088, 4099, 64, "bf16")])
+                                            (1, 256, 129, 64, "bf16"), (16, 1088, 4099, 64, "bf16"),
+                                            (32, 1024, 3001, 64, "bf16"), (24, 2048, 777, 128, "f16"),
+                                            (16, 5120, 20000, 64, "bf16")])
 def test_lmhead_fused_matches_oracle(dev, M, K, V, gs, dtype):
     import torch
 
@@ -141,10 +143,11 @@ def test_lmhead_fused_matches_oracle(dev, M, K, V, gs, dtype):
     assert int(res2.accept_len.item()) == a and int(res2.bonus.item()) == bonus
 
 
-def test_lmhead_exact_ties_pick_lowest_index(dev):
+@pytest.mark.parametrize("K", [256, 512])  # general and streaming main loops
+def test_lmhead_exact_ties_pick_lowest_index(dev, K):
     from dflash_mlx_amd.lm_head import lm_head_greedy_accept
 
-    M, K, V, gs = 16, 256, 700, 64
+    M, V, gs = 16, 700, 64
     x, w_q, s, b = _lm_case(M, K, V, gs, seed=11)
     # positive activations; rows 333 and 91 get identical weights and a large
     # bias, so both hold the row maximum exactly (an exact tie)

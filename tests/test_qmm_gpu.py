@@ -119,13 +119,15 @@ def test_closed_form_exact(dev):
     x = oracle.f32_to_bf16_bits(xf)
     want = oracle.quantized_matmul(x, w_q, s, b, group_size=gs, out_dtype="bf16")
     for tuning in (None, (1, 1, 1, 0), (1, 2, 4, 0), (1, 4, 8, 0), (1, 1, 3, 0), (2, 1, 0, 1),
-                   (2, 2, 0, 1), (2, 1, 0, 3), (2, 2, 0, 2)):
+                   (2, 2, 0, 1), (2, 1, 0, 3), (2, 2, 0, 2), (3, 1, 1, 0), (3, 2, 4, 0),
+                   (3, 4, 3, 0), (3, 1, 8, 0)):
         got = _run(dev, x, w_q, s, b, gs, tuning=_tuning(tuning))
         assert np.array_equal(got, want), f"tuning {tuning}"
 
 
 def _tuning(t):
-    """(path, tiles_per_wave, waves_per_block, k_splits); path 1 general, 2 streaming."""
+    """(path, tiles_per_wave, waves_per_block, k_splits); path 1 general, 2 streaming,
+    3 register-direct."""
     if t is None:
         return None
     from dflash_mlx_amd import _lib
@@ -151,6 +153,32 @@ def test_streaming_kernel_shapes(dev, M, gs):
     x, w_q, s, b = make_qmm_case(M, K, N, gs, seed=M * 3 + gs)
     for t in ((2, 0, 0, 1), (2, 0, 0, 3), (2, 2, 0, 2)):
         _check(_run(dev, x, w_q, s, b, gs, tuning=_tuning(t)), x, w_q, s, b, gs)
+
+
+@pytest.mark.parametrize("M", [1, 4, 8, 13, 16])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+def test_direct_kernel_shapes(dev, M, gs):
+    # forced onto the register-direct kernel: every tile count, K split and a
+    # ragged N (the last workgroup's rows past N are clamped loads, never stored)
+    K, N = 2048, 632
+    x, w_q, s, b = make_qmm_case(M, K, N, gs, seed=M * 5 + gs)
+    for t in ((3, 1, 1, 0), (3, 2, 3, 0), (3, 4, 8, 0), (3, 1, 5, 0)):
+        _check(_run(dev, x, w_q, s, b, gs, tuning=_tuning(t)), x, w_q, s, b, gs)
+
+
+@pytest.mark.parametrize("gs", [32, 64, 128])
+def test_direct_kernel_f16(dev, gs):
+    M, K, N = 16, 1536, 520
+    x, w_q, s, b = make_qmm_case(M, K, N, gs, dtype="f16", seed=gs + 1)
+    for t in ((3, 1, 2, 0), (3, 2, 6, 0)):
+        _check(_run(dev, x, w_q, s, b, gs, "f16", tuning=_tuning(t)), x, w_q, s, b, gs, "f16")
+
+
+@pytest.mark.parametrize("K,N", [(4096, 4096), (4096, 1024), (4096, 12288), (12288, 4096),
+                                 (5120, 17408), (17408, 5120)])
+def test_direct_kernel_layer_shapes(dev, K, N):
+    x, w_q, s, b = make_qmm_case(16, K, N, 64, seed=K + N)
+    _check(_run(dev, x, w_q, s, b, 64, tuning=_tuning((3, 0, 0, 0))), x, w_q, s, b, 64)
 
 
 def test_deterministic_and_workspace_reuse(dev):
