@@ -283,10 +283,24 @@ struct Direct {
 #pragma unroll
     for (int t = 0; t < NT; ++t) accb[t] = zero4();
     Step A, B;
+    if (i1 - i0 <= 2) {
+      // short range: every load of the wavefront in one round trip
+      XStep XA, XB;
+      load(A, c, i0);
+      load_x(XA, c, i0);
+      if (i1 - i0 == 2) {
+        load(B, c, i0 + 1);
+        load_x(XB, c, i0 + 1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      compute(A, XA, c, acc, accb, sel, dq);
+      if (i1 - i0 == 2) compute(B, XB, c, acc, accb, sel, dq);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) acc[t] += accb[t];
+      return;
+    }
     load(A, c, i0);
-    if (i1 - i0 == 1) {
-      step(A, c, i0, acc, accb, sel, dq);
-    } else {
+    {
       load(B, c, i0 + 1);
       __builtin_amdgcn_sched_barrier(0);
       int i = i0;

@@ -194,6 +194,7 @@ __global__ __launch_bounds__(64 * WV) void lmhead_stream_kernel(LmArgs a) {
   cx.n0 = blockIdx.x * S::NB;
   cx.lane = tid & 63;
   cx.wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  cx.dense();
   f32x4 acc[S::NT][MT];
 #pragma unroll
   for (int t = 0; t < S::NT; ++t)

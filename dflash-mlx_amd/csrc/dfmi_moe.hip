@@ -4,17 +4,25 @@
 // Pairs p < P map (activation row lhs_rows[p], expert rhs_experts[p]).  A run
 // is a maximal stretch of consecutive pairs with the same expert (after the
 // sort mlx-lm's SwitchGLU applies for >= 64 pairs, every expert is one run;
-// unsorted pairs just make shorter runs).  Grid: (N blocks of 16*NT rows, P);
-// the workgroup of the first pair of a run streams that expert's weight rows
-// once for the whole run, 16 gathered activation rows per MFMA block, and the
-// other pairs' workgroups exit at once.  The main loop is the general one
-// (Core: wavefronts split K, partial tiles summed through LDS), with the
-// activation row of each MFMA lane taken from lhs_rows.
+// unsorted pairs just make shorter runs).  Grid: (column blocks, P); the
+// workgroup of the first pair of a run streams that expert's weight rows once
+// for the whole run, 16 gathered activation rows per MFMA block, and the
+// other pairs' workgroups exit at once.
+//
+//  * gather_stream_kernel (K a multiple of 256 and of 8 groups): the
+//    streaming main loop (LDS-DMA staging of whole weight lines, 4
+//    wavefronts) over a 64-row block: 64 rows of one expert, or for the fused
+//    SwiGLU 32 gate rows and the same 32 up rows, so one workgroup produces
+//    32 finished h columns.  The activation DMA takes its rows from lhs_rows.
+//  * gather_kernel (every other shape): the general main loop (Core:
+//    wavefronts split K, partial tiles summed through LDS), with the
+//    activation row of each MFMA lane taken from lhs_rows.
 #include <algorithm>
 #include <cmath>
 
 #include "dfmi_core.h"
 #include "dfmi_host.h"
+#include "dfmi_stream.h"
 
 namespace dfmi {
 
@@ -133,6 +141,131 @@ __global__ __launch_bounds__(kMaxWaves * 64) void gather_kernel(GatherArgs a) {
   }
 }
 
+template <typename Tag, int GS, bool GLU>
+__global__ __launch_bounds__(256) void gather_stream_kernel(GatherArgs a) {
+  using S = Stream<Tag, GS, 1, 4>;
+  constexpr int OUTC = GLU ? S::NB / 2 : S::NB;  // output columns per workgroup
+  __shared__ int32_t s_rows[16];   // activation row of each MFMA row (clamped)
+  __shared__ int32_t s_lhs[16];    // raw lhs ids of the current 16 pairs
+  __shared__ int32_t s_rhs[18];    // rhs[p-1 .. p+16]
+  const int p = blockIdx.y;
+  const int tid = threadIdx.x;
+  // One memory round trip for all the indexing: the expert ids around p and
+  // the activation rows of the first 16 pairs, loaded together.
+  if (tid < 18) {
+    const int q = p - 1 + tid;
+    s_rhs[tid] = (q >= 0 && q < a.P) ? a.rhs[q] : 0;
+  } else if (tid >= 64 && tid < 80) {
+    const int q = min(p + tid - 64, a.P - 1);
+    s_lhs[tid - 64] = a.lhs ? a.lhs[q] : q;
+  }
+  __syncthreads();
+  const int e = s_rhs[1];
+  if (p > 0 && s_rhs[0] == e) return;  // not the first pair of its run (uniform)
+  int run = 1;
+  while (p + run < a.P && run < 17 && s_rhs[1 + run] == e) ++run;
+  if (run == 17)  // a run longer than the window: rare, continue in memory
+    while (p + run < a.P && a.rhs[p + run] == e) ++run;
+  const bool bad_e = e < 0 || e >= a.E;
+  const size_t ee = bad_e ? 0 : (size_t)e;
+  const uint32_t wbytes = (uint32_t)a.N * (uint32_t)(a.K / 2);
+  const uint32_t sbytes = (uint32_t)a.N * (uint32_t)(a.K / GS) * 2u;
+  typename S::Ctx cx;
+  cx.x = buffer_rsrc(a.x, (uint32_t)a.x_rows * (uint32_t)a.K * 2u);
+  cx.w = buffer_rsrc(a.w[0] + ee * (wbytes / 4), wbytes);
+  cx.s = buffer_rsrc(a.s[0] + ee * (sbytes / 2), sbytes);
+  cx.b = buffer_rsrc(a.b[0] + ee * (sbytes / 2), sbytes);
+  cx.w2 = buffer_rsrc(a.w[1] + ee * (wbytes / 4), wbytes);
+  cx.s2 = buffer_rsrc(a.s[1] + ee * (sbytes / 2), sbytes);
+  cx.b2 = buffer_rsrc(a.b[1] + ee * (sbytes / 2), sbytes);
+  cx.split = GLU ? OUTC : S::NB;
+  cx.xrows = s_rows;
+  cx.xbase = 0;
+  cx.K = a.K;
+  cx.N = a.N;
+  cx.groups = a.K / GS;
+  cx.n0 = blockIdx.x * OUTC;
+  cx.lane = tid & 63;
+  cx.wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  float* red = reinterpret_cast<float*>(dfmi_smem);
+  for (int g0 = 0; g0 < run; g0 += 16) {
+    const int rows = min(16, run - g0);
+    if (g0 > 0 && tid < 16) {  // later row blocks of a long run
+      const int pp = p + g0 + min(tid, rows - 1);
+      s_lhs[tid] = a.lhs ? a.lhs[pp] : pp;
+    }
+    __syncthreads();
+    if (tid < 16) {
+      // rows past the run repeat its last pair; invalid ids read row 0 and
+      // are reported as NaN below
+      int xr = s_lhs[min(tid, rows - 1)];
+      if (xr < 0 || xr >= a.x_rows) xr = 0;
+      s_rows[tid] = xr;
+    }
+    __syncthreads();
+    cx.M = rows;
+    f32x4 acc[S::NT][1];
+#pragma unroll
+    for (int t = 0; t < S::NT; ++t) acc[t][0] = zero4();
+    if (!bad_e) S::run(cx, 0, a.K / S::CK, acc);
+    // sum the 4 wavefronts' partial tiles through LDS (every DMA has landed)
+    __syncthreads();
+    {
+      float* mine = red + cx.wave * S::RED_FLOATS;
+#pragma unroll
+      for (int t = 0; t < S::NT; ++t)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) mine[(t * 4 + j) * 64 + cx.lane] = acc[t][0][j];
+    }
+    __syncthreads();
+    constexpr int OUT = OUTC * 16;  // output elements: tiles 0 .. OUTC/16-1
+    for (int el = tid; el < OUT; el += 256) {
+      float v = 0.f, u = 0.f;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        v += red[w * S::RED_FLOATS + el];
+        if (GLU) u += red[w * S::RED_FLOATS + OUT + el];  // up tile t + OUTC/16
+      }
+      const int l = el & 63, j = (el >> 6) & 3, t = el >> 8;
+      const int m = 4 * (l >> 4) + j;
+      const int n = cx.n0 + t * 16 + (l & 15);
+      if (m < rows && n < a.N) {
+        const int pp = p + g0 + m;
+        const int xrow = s_lhs[m];
+        float out;
+        if (bad_e || xrow < 0 || xrow >= a.x_rows) {
+          out = __builtin_nanf("");
+        } else if (GLU) {
+          out = silu_mul<Tag>(rnd<Tag>(v), rnd<Tag>(u));
+        } else {
+          out = v;
+        }
+        a.y[(int64_t)pp * a.N + n] = Num<Tag>::f2h(out);
+      }
+    }
+    __syncthreads();  // s_lhs, s_rows and the LDS stages are reused by the next row block
+  }
+}
+
+template <typename Tag, int GS, bool GLU>
+static void launch_gather_stream_t(const GatherArgs& a, hipStream_t st) {
+  using S = Stream<Tag, GS, 1, 4>;
+  constexpr int OUTC = GLU ? S::NB / 2 : S::NB;
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(&gather_stream_kernel<Tag, GS, GLU>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, S::LDS_BYTES);
+  (void)attr;
+  const dim3 grid((unsigned)((a.N + OUTC - 1) / OUTC), (unsigned)a.P);
+  hipLaunchKernelGGL((gather_stream_kernel<Tag, GS, GLU>), grid, dim3(256), S::LDS_BYTES, st, a);
+}
+
+template <typename Tag, bool GLU>
+static void launch_gather_stream(const GatherArgs& a, int gs, hipStream_t st) {
+  if (gs == 32) launch_gather_stream_t<Tag, 32, GLU>(a, st);
+  else if (gs == 64) launch_gather_stream_t<Tag, 64, GLU>(a, st);
+  else launch_gather_stream_t<Tag, 128, GLU>(a, st);
+}
+
 template <typename Tag, int GS, int NT, bool KFULL, bool GLU>
 static void launch_gather_t(const GatherArgs& a, int n_blocks, int waves, hipStream_t st) {
   hipLaunchKernelGGL((gather_kernel<Tag, GS, NT, KFULL, GLU>), dim3(n_blocks, a.P),
@@ -221,11 +354,23 @@ static int gather_common(const void* x, int x_dtype, int64_t x_rows, const uint3
   a.N = (int)N;
   a.E = (int)E;
   a.chunks = (int)((K + kChunkK - 1) / kChunkK);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  // streaming loop: whole 256-k steps and scale blocks, 32-bit buffer offsets
+  // per expert and for the activations
+  if (stream_eligible(16, K, N, group_size) && x_rows * K * 2 < (1ll << 31)) {
+    if (glu) {
+      if (x_dtype == DFMI_BF16) launch_gather_stream<BF16, true>(a, group_size, st);
+      else launch_gather_stream<F16, true>(a, group_size, st);
+    } else {
+      if (x_dtype == DFMI_BF16) launch_gather_stream<BF16, false>(a, group_size, st);
+      else launch_gather_stream<F16, false>(a, group_size, st);
+    }
+    return check_launch(glu ? "dfmi_gather_qmm_swiglu" : "dfmi_gather_qmm_affine");
+  }
   const bool kfull = (K % kChunkK) == 0;
   const int nt = N >= 1024 ? 2 : 1;
   const int n_blocks = (int)((N + 16 * nt - 1) / (16 * nt));
   const int waves = std::max(1, std::min(kMaxWaves, a.chunks));
-  hipStream_t st = static_cast<hipStream_t>(stream);
   if (glu) {
     if (x_dtype == DFMI_BF16) launch_gather<BF16, true>(a, group_size, kfull, nt, n_blocks, waves, st);
     else launch_gather<F16, true>(a, group_size, kfull, nt, n_blocks, waves, st);

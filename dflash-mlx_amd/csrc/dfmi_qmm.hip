@@ -191,6 +191,7 @@ __global__ __launch_bounds__(64 * WV) void qmm_stream_kernel(StreamArgs a) {
   cx.n0 = nb * S::NB;
   cx.lane = threadIdx.x & 63;
   cx.wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  cx.dense();
   const int c0 = (int)((int64_t)kpi * a.chunks / a.kp);
   const int c1 = (int)((int64_t)(kpi + 1) * a.chunks / a.kp);
   f32x4 acc[S::NT][MT];

@@ -131,10 +131,26 @@ struct Stream {
 
   struct Ctx {
     __amdgpu_buffer_rsrc_t x, w, s, b;  // activations, packed weights, scales, biases
+    // Rows >= split of the block come from a second weight set (row - split):
+    // the up projection next to the gate projection of a fused SwiGLU.
+    __amdgpu_buffer_rsrc_t w2, s2, b2;
+    const int32_t* xrows;  // activation row of local row m: xrows[m], or xbase + m if null
+    int xbase;
+    int split;   // NB: one weight set
     int K, M, N;
     int groups;  // K / GS
-    int n0;      // first weight row of this workgroup
+    int n0;      // first weight row of this workgroup (in each weight set)
     int wave, lane;
+
+    // Dense defaults: activation rows 0 .. M-1, one weight set.
+    __device__ inline void dense() {
+      xrows = nullptr;
+      xbase = 0;
+      split = NB;
+      w2 = w;
+      s2 = s;
+      b2 = b;
+    }
   };
 
   // Lane-constant offsets, computed once.
@@ -172,7 +188,8 @@ struct Stream {
       const int r = j * (64 / XPPR) + cx.lane / XPPR;
       const int piece = (cx.lane % XPPR) ^ (r & 15);
       const int m = min(r, cx.M - 1);
-      L.xg[i] = (uint32_t)m * (uint32_t)cx.K * 2u + (uint32_t)piece * 16u;
+      const int xr = cx.xrows ? cx.xrows[m] : cx.xbase + m;
+      L.xg[i] = (uint32_t)xr * (uint32_t)cx.K * 2u + (uint32_t)piece * 16u;
     }
     // weight stage: instruction i of wavefront w covers 64 / WPPR consecutive
     // rows; lane l loads piece (l % WPPR) ^ (row % WPPR) of its row into slot
@@ -182,7 +199,7 @@ struct Stream {
     for (int i = 0; i < W_DMA; ++i) {
       const int r = (cx.wave * W_DMA + i) * RPI + cx.lane / WPPR;
       const int piece = (cx.lane % WPPR) ^ (r % WPPR);
-      const int n = min(cx.n0 + r, cx.N - 1);
+      const int n = min(cx.n0 + (r >= cx.split ? r - cx.split : r), cx.N - 1);
       L.wg[i] = (uint32_t)n * (uint32_t)(cx.K / 2) + (uint32_t)piece * 16u;
     }
     // fragment reads (row m = col of M-block 0, row r = col of tile 0; the
@@ -210,9 +227,11 @@ struct Stream {
     const uint32_t u = (uint32_t)c * (uint32_t)(CK / 2);
     constexpr int RPI = 64 / WPPR;
 #pragma unroll
-    for (int i = 0; i < W_DMA; ++i)
-      dma16(cx.w, L.wg[i], u,
-            dfmi_smem + W_OFF + stage * WBUF + (cx.wave * W_DMA + i) * RPI * WROW);
+    for (int i = 0; i < W_DMA; ++i) {
+      const int r0 = (cx.wave * W_DMA + i) * RPI;  // wave-uniform
+      dma16(r0 >= cx.split ? cx.w2 : cx.w, L.wg[i], u,
+            dfmi_smem + W_OFF + stage * WBUF + r0 * WROW);
+    }
   }
 
   // Scale / bias block sb = groups [32 sb, 32 sb + 32) of every row, laid
@@ -230,10 +249,12 @@ struct Stream {
       const int r0 = (j & 3) * 16;
       const int r = r0 + (cx.lane >> 2);
       const int q = (cx.lane & 3) ^ ((r >> 2) & 3);
-      const int n = min(cx.n0 + r, cx.N - 1);
+      const bool second = r0 >= cx.split;  // wave-uniform
+      const int n = min(cx.n0 + (second ? r - cx.split : r), cx.N - 1);
       const int piece = min(sb * 4 + q, last_piece);
       const uint32_t off = ((uint32_t)n * (uint32_t)cx.groups + (uint32_t)piece * 8u) * 2u;
-      dma16(arr ? cx.b : cx.s, off, 0u, dfmi_smem + SB_OFF + buf * SBBUF + arr * 4096 + r0 * 64);
+      const __amdgpu_buffer_rsrc_t src = arr ? (second ? cx.b2 : cx.b) : (second ? cx.s2 : cx.s);
+      dma16(src, off, 0u, dfmi_smem + SB_OFF + buf * SBBUF + arr * 4096 + r0 * 64);
     }
   }
 

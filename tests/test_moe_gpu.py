@@ -88,14 +88,15 @@ def test_gather_qmm_shapes(dev, K, N):
     _check(from_dev(got, "bf16"), want, "bf16")
 
 
-def test_gather_qmm_long_runs(dev):
+@pytest.mark.parametrize("K", [256, 512])  # general and streaming main loops
+def test_gather_qmm_long_runs(dev, K):
     """Runs of more than 16 pairs on one expert (several MFMA row blocks), and
     lhs_indices=None (row p for pair p)."""
     import torch
 
     from dflash_mlx_amd.moe import gather_qmm
 
-    E, N, K = 4, 64, 256
+    E, N = 4, 64
     rhs = np.array([1] * 37 + [3] * 5 + [0] * 17 + [2])
     P = rhs.shape[0]
     wq, s, b = _experts(E, N, K, 64, "bf16", seed=9)
@@ -106,12 +107,13 @@ def test_gather_qmm_long_runs(dev):
     _check(from_dev(got, "bf16"), want, "bf16")
 
 
-def test_gather_qmm_invalid_ids_give_nan_rows(dev):
+@pytest.mark.parametrize("K", [256, 512])  # general and streaming main loops
+def test_gather_qmm_invalid_ids_give_nan_rows(dev, K):
     import torch
 
     from dflash_mlx_amd.moe import gather_qmm
 
-    E, N, K, R = 3, 32, 256, 4
+    E, N, R = 3, 32, 4
     wq, s, b = _experts(E, N, K, 64, "bf16", seed=1)
     x = _x(R, K, "bf16", seed=2)
     rhs = np.array([0, 7, 1, -1, 2, 2])
@@ -127,7 +129,8 @@ def test_gather_qmm_invalid_ids_give_nan_rows(dev):
     _check(from_dev(got, "bf16")[good], want, "bf16")
 
 
-@pytest.mark.parametrize("T,k,E,D,I", [(4, 2, 8, 256, 128), (16, 8, 32, 2048, 512)])
+@pytest.mark.parametrize("T,k,E,D,I", [(4, 2, 8, 256, 128), (16, 8, 32, 2048, 512),
+                                       (5, 3, 6, 1024, 192)])
 def test_switch_glu_matches_oracle(dev, T, k, E, D, I):
     import torch
 
