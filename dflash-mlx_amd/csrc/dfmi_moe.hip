@@ -9,7 +9,7 @@
 // for the whole run, 16 gathered activation rows per MFMA block, and the
 // other pairs' workgroups exit at once.
 //
-//  * gather_stream_kernel (K a multiple of 256 and of 8 groups): the
+//  * gather_stream_kernel (K >= 1024, a multiple of 256 and of 8 groups): the
 //    streaming main loop (LDS-DMA staging of whole weight lines, 4
 //    wavefronts) over a 64-row block: 64 rows of one expert, or for the fused
 //    SwiGLU 32 gate rows and the same 32 up rows, so one workgroup produces
@@ -356,8 +356,11 @@ static int gather_common(const void* x, int x_dtype, int64_t x_rows, const uint3
   a.chunks = (int)((K + kChunkK - 1) / kChunkK);
   hipStream_t st = static_cast<hipStream_t>(stream);
   // streaming loop: whole 256-k steps and scale blocks, 32-bit buffer offsets
-  // per expert and for the activations
-  if (stream_eligible(16, K, N, group_size) && x_rows * K * 2 < (1ll << 31)) {
+  // per expert and for the activations.  Measured on MI355X (16 tokens, top-8
+  // of 256 experts): equal to the general loop for the SwiGLU pair at K = 2048
+  // and slower for K = 512 (two steps per workgroup do not amortise its
+  // pipeline fill), so short K stays on the general loop.
+  if (stream_eligible(16, K, N, group_size) && K >= 1024 && x_rows * K * 2 < (1ll << 31)) {
     if (glu) {
       if (x_dtype == DFMI_BF16) launch_gather_stream<BF16, true>(a, group_size, st);
       else launch_gather_stream<F16, true>(a, group_size, st);

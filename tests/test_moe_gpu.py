@@ -88,7 +88,7 @@ def test_gather_qmm_shapes(dev, K, N):
     _check(from_dev(got, "bf16"), want, "bf16")
 
 
-@pytest.mark.parametrize("K", [256, 512])  # general and streaming main loops
+@pytest.mark.parametrize("K", [256, 1024])  # general and streaming main loops
 def test_gather_qmm_long_runs(dev, K):
     """Runs of more than 16 pairs on one expert (several MFMA row blocks), and
     lhs_indices=None (row p for pair p)."""
@@ -107,7 +107,7 @@ def test_gather_qmm_long_runs(dev, K):
     _check(from_dev(got, "bf16"), want, "bf16")
 
 
-@pytest.mark.parametrize("K", [256, 512])  # general and streaming main loops
+@pytest.mark.parametrize("K", [256, 1024])  # general and streaming main loops
 def test_gather_qmm_invalid_ids_give_nan_rows(dev, K):
     import torch
 
