@@ -322,12 +322,20 @@ def run_lmhead(args, torch):
         del w
     h = torch.randn((M, K), generator=gen, device=dev).to(torch.bfloat16)
     ids = torch.randint(0, V, (M,), generator=gen, device=dev, dtype=torch.int32)
+    # two weight copies (875 MB > the 256 MB infinity cache), four calls per
+    # graph replay, so the figure is a call's steady-state time and not one
+    # graph launch per call
+    heads = [(w_q, s, b), (w_q.clone(), s.clone(), b.clone())]
+    R = 4
 
     def fn():
-        lm_head_greedy_accept(h, w_q, s, b, verify_ids=ids, group_size=64)
+        for r in range(R):
+            wq_r, s_r, b_r = heads[r % 2]
+            lm_head_greedy_accept(h, wq_r, s_r, b_r, verify_ids=ids, group_size=64)
 
     g = graph_of(torch, fn)
-    ms = time_replays(torch, g, args.steps, warmup=args.warmup)
+    ms_step = time_replays(torch, g, args.steps, warmup=args.warmup)  # one step = R calls
+    ms = ms_step / R
     nbytes = V * K // 2 + 4 * V * K // 64 + 2 * M * K + 12 * M
     gbs = nbytes / (ms * 1e-3) / 1e9
     roofline = {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -336,8 +344,8 @@ def run_lmhead(args, torch):
                 "kernel": "lmhead_stream_kernel", "bytes_per_launch": nbytes,
                 "us_per_launch": round(ms * 1e3, 3)}
     config = {"workload": "fused lm_head [16,5120]x[151936,5120] int4 gs64 + greedy + accept",
-              "M": M, "K": K, "V": V}
-    return base_result(args, gbs, ms, 1, config, roofline)
+              "M": M, "K": K, "V": V, "calls_per_step": R}
+    return base_result(args, gbs, ms_step, R, config, roofline)
 
 
 def run_moe(args, torch):
@@ -372,6 +380,7 @@ def run_moe(args, torch):
         lhs = (order // k).to(torch.int32)
         inv = torch.empty_like(order)
         inv[order] = torch.arange(order.numel(), device=dev)
+        inv = inv.to(torch.int32)  # row of each pair in the expert-sorted outputs
         n_e = int(torch.unique(flat).numel())
         total += n_e * 3 * (I * D // 2 + 4 * I * D // 64) + 2 * T * D * 2
         x = torch.randn((T, D), generator=gen, device=dev).to(torch.bfloat16)
@@ -382,7 +391,7 @@ def run_moe(args, torch):
         for (gate, up, down, rhs, lhs, inv, sc, x) in lay:
             h = gather_swiglu(x, gate, up, rhs, lhs_indices=lhs, group_size=64)
             y = gather_qmm(h, *down, rhs, group_size=64)
-            moe_combine(y[inv], sc)
+            moe_combine(y, sc, y_rows=inv)
 
     g = graph_of(torch, fn)
     ms = time_replays(torch, g, args.steps, warmup=args.warmup)

@@ -56,8 +56,8 @@ _SIGNATURES = {
     "dfmi_gather_qmm_swiglu": (_int, [_c_void_p, _int, _i64, _c_void_p, _c_void_p, _c_void_p,
                                       _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                       _c_void_p, _i64, _i64, _i64, _i64, _int, _int, _c_void_p]),
-    "dfmi_moe_combine": (_int, [_c_void_p, _int, _c_void_p, _c_void_p, _i64, _i64, _i64,
-                                _c_void_p]),
+    "dfmi_moe_combine": (_int, [_c_void_p, _int, _c_void_p, _c_void_p, _c_void_p, _i64, _i64,
+                                _i64, _c_void_p]),
     "dfmi_greedy_accept": (_int, [_c_void_p, _int, _c_void_p, _c_void_p, _i64, _i64, _c_void_p,
                                   _c_void_p, _c_void_p, _c_void_p, _size, _c_void_p]),
     "dfmi_greedy_workspace_bytes": (_size, [_i64]),

@@ -384,16 +384,24 @@ static int gather_common(const void* x, int x_dtype, int64_t x_rows, const uint3
   return check_launch(glu ? "dfmi_gather_qmm_swiglu" : "dfmi_gather_qmm_affine");
 }
 
-// out[t, d] = rnd(sum_j scores[t, j] * y[t*k + j, d]), fp32, j in order
+// out[t, d] = rnd(sum_j scores[t, j] * y[r(t*k + j), d]), fp32, j in order;
+// r(p) = y_rows[p] (the pair's row in a sorted y: the unsort mlx-lm's
+// SwitchGLU applies before the weighted sum) or p.  A row id outside
+// [0, T*k) makes the output NaN.
 template <typename Tag>
-__global__ __launch_bounds__(256) void combine_kernel(const uint16_t* y, const float* scores,
-                                                      uint16_t* out, int T, int k, int D) {
+__global__ __launch_bounds__(256) void combine_kernel(const uint16_t* y, const int32_t* y_rows,
+                                                      const float* scores, uint16_t* out, int T,
+                                                      int k, int D) {
   const int t = blockIdx.y;
+  const int64_t P = (int64_t)T * k;
   for (int d = blockIdx.x * 256 + threadIdx.x; d < D; d += gridDim.x * 256) {
     float acc = 0.f;
-    for (int j = 0; j < k; ++j)
-      acc = __builtin_fmaf(scores[(int64_t)t * k + j],
-                           Num<Tag>::h2f(y[((int64_t)t * k + j) * D + d]), acc);
+    for (int j = 0; j < k; ++j) {
+      const int64_t p = (int64_t)t * k + j;
+      const int64_t r = y_rows ? (int64_t)y_rows[p] : p;
+      const float v = (r >= 0 && r < P) ? Num<Tag>::h2f(y[r * D + d]) : __builtin_nanf("");
+      acc = __builtin_fmaf(scores[p], v, acc);
+    }
     out[(int64_t)t * D + d] = Num<Tag>::f2h(acc);
   }
 }
@@ -422,8 +430,9 @@ extern "C" int dfmi_gather_qmm_swiglu(const void* x, int x_dtype, int64_t x_rows
                        lhs_rows, rhs_experts, h, P, K, N, E, group_size, bits, true, stream);
 }
 
-extern "C" int dfmi_moe_combine(const void* y, int y_dtype, const float* scores, void* out,
-                                int64_t T, int64_t k, int64_t D, void* stream) {
+extern "C" int dfmi_moe_combine(const void* y, int y_dtype, const int32_t* y_rows,
+                                const float* scores, void* out, int64_t T, int64_t k, int64_t D,
+                                void* stream) {
   if (y_dtype != DFMI_BF16 && y_dtype != DFMI_F16) {
     set_error("dfmi_moe_combine: dtype %d unsupported (bf16 or f16)", y_dtype);
     return DFMI_EINVAL;
@@ -442,11 +451,11 @@ extern "C" int dfmi_moe_combine(const void* y, int y_dtype, const float* scores,
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (y_dtype == DFMI_BF16)
     hipLaunchKernelGGL(combine_kernel<BF16>, dim3(gx, (unsigned)T), dim3(256), 0, st,
-                       static_cast<const uint16_t*>(y), scores, static_cast<uint16_t*>(out),
-                       (int)T, (int)k, (int)D);
+                       static_cast<const uint16_t*>(y), y_rows, scores,
+                       static_cast<uint16_t*>(out), (int)T, (int)k, (int)D);
   else
     hipLaunchKernelGGL(combine_kernel<F16>, dim3(gx, (unsigned)T), dim3(256), 0, st,
-                       static_cast<const uint16_t*>(y), scores, static_cast<uint16_t*>(out),
-                       (int)T, (int)k, (int)D);
+                       static_cast<const uint16_t*>(y), y_rows, scores,
+                       static_cast<uint16_t*>(out), (int)T, (int)k, (int)D);
   return check_launch("dfmi_moe_combine");
 }

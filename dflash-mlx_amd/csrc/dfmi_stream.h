@@ -47,6 +47,7 @@ namespace dfmi {
 
 constexpr int kStreamRows = 64;   // weight rows per workgroup
 constexpr int kStreamTiles = 4;   // 16-row MFMA tiles per workgroup, all in every wavefront
+constexpr uint32_t kNoRow = 0x80000000u;  // buffer offset of an activation row past M
 
 // Wait until at most N vector-memory operations of this wavefront are
 // outstanding and all LDS operations are done, then the workgroup barrier.
@@ -180,8 +181,11 @@ struct Stream {
     Lane L;
     const int col = cx.lane & 15, kg = cx.lane >> 4;
     // activation stage: instruction j covers 64 / XPPR consecutive rows; lane
-    // l loads piece (l % XPPR) ^ (row & 15) of its row into slot l % XPPR;
-    // rows >= M re-read row M-1 (their outputs are never stored)
+    // l loads piece (l % XPPR) ^ (row & 15) of its row into slot l % XPPR.
+    // Rows >= M take an offset past the end of the buffer: the range check
+    // returns zeros without a memory request (their outputs are never
+    // stored).  kNoRow + any step offset stays below 2^32, and every x
+    // buffer the kernels take is smaller than 2^31 bytes.
 #pragma unroll
     for (int i = 0; i < X_DMA; ++i) {
       const int j = cx.wave * X_DMA + i;
@@ -189,7 +193,7 @@ struct Stream {
       const int piece = (cx.lane % XPPR) ^ (r & 15);
       const int m = min(r, cx.M - 1);
       const int xr = cx.xrows ? cx.xrows[m] : cx.xbase + m;
-      L.xg[i] = (uint32_t)xr * (uint32_t)cx.K * 2u + (uint32_t)piece * 16u;
+      L.xg[i] = r < cx.M ? (uint32_t)xr * (uint32_t)cx.K * 2u + (uint32_t)piece * 16u : kNoRow;
     }
     // weight stage: instruction i of wavefront w covers 64 / WPPR consecutive
     // rows; lane l loads piece (l % WPPR) ^ (row % WPPR) of its row into slot

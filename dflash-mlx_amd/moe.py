@@ -110,20 +110,31 @@ def gather_swiglu(x: torch.Tensor, gate: Triple, up: Triple, rhs_indices: torch.
     return h
 
 
-def moe_combine(y: torch.Tensor, scores: torch.Tensor) -> torch.Tensor:
-    """``out[t] = sum_j scores[t, j] * y[t*k + j]`` (fp32 accumulate, j in
-    order), ``y`` ``[T*k, D]``, ``scores`` ``[T, k]`` -> ``[T, D]``."""
+def moe_combine(y: torch.Tensor, scores: torch.Tensor, *,
+                y_rows: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``out[t] = sum_j scores[t, j] * y[r(t*k + j)]`` (fp32 accumulate, j in
+    order), ``y`` ``[T*k, D]``, ``scores`` ``[T, k]`` -> ``[T, D]``.
+
+    ``r(p) = y_rows[p]`` when given, else ``p``: with ``y`` in expert-sorted
+    pair order (what ``gather_qmm`` returns for sorted pairs), ``y_rows`` is
+    the inverse of the sort permutation, i.e. mlx-lm SwitchGLU's unsort
+    folded into the weighted sum of the Qwen MoE block
+    (dflash_mlx/engine/target_qwen_gdn.py:865,874)."""
     _runtime.require_device(y, "y")
     _runtime.require_device(scores, "scores")
     T, k = int(scores.shape[0]), int(scores.shape[1])
     D = int(y.shape[-1])
     if int(y.numel()) != T * k * D:
         raise ValueError("y must hold T*k rows of D")
+    rows = _indices(y_rows, "y_rows")
+    if rows is not None and int(rows.numel()) != T * k:
+        raise ValueError("y_rows must hold T*k row ids")
     yc = y.reshape(T * k, D).contiguous()
     sc = scores.to(torch.float32).contiguous()
     out = torch.empty((T, D), dtype=y.dtype, device=y.device)
     lib = _lib.load()
-    _lib.check(lib.dfmi_moe_combine(yc.data_ptr(), _runtime.dtype_code(y.dtype), sc.data_ptr(),
+    _lib.check(lib.dfmi_moe_combine(yc.data_ptr(), _runtime.dtype_code(y.dtype),
+                                    rows.data_ptr() if rows is not None else None, sc.data_ptr(),
                                     out.data_ptr(), T, k, D, _runtime.stream_ptr(y.device)),
                "dfmi_moe_combine")
     return out

@@ -137,12 +137,17 @@ int dfmi_gather_qmm_swiglu(const void *x, int x_dtype, int64_t x_rows,
 
 /*
  * Weighted sum over each token's top-k expert outputs (the Qwen MoE block's
- * `(y * scores[..., None]).sum(axis=-2)`):
- *   out[t, D] = rnd(sum_j scores[t, j] * y[t*k + j, D])   (fp32 accumulate)
- * y and out in y_dtype; scores fp32 [T, k].
+ * `(y * scores[..., None]).sum(axis=-2)`, reached from
+ * dflash_mlx/engine/target_qwen_gdn.py:865,874), with the unsort mlx-lm's
+ * SwitchGLU applies to expert-sorted outputs folded in:
+ *   out[t, D] = rnd(sum_j scores[t, j] * y[r(t*k + j), D])   (fp32 accumulate)
+ * r(p) = y_rows[p] when y_rows != NULL (y in expert-sorted pair order,
+ * y_rows = the inverse of the sort permutation), else p.  A row id outside
+ * [0, T*k) gives NaN outputs for that token.  y and out in y_dtype; scores
+ * fp32 [T, k].
  */
-int dfmi_moe_combine(const void *y, int y_dtype, const float *scores, void *out, int64_t T,
-                     int64_t k, int64_t D, void *stream);
+int dfmi_moe_combine(const void *y, int y_dtype, const int32_t *y_rows, const float *scores,
+                     void *out, int64_t T, int64_t k, int64_t D, void *stream);
 
 /*
  * Greedy verify over given logits: posterior[m] = argmax_v masked(logits[m, v])

@@ -69,7 +69,7 @@ def test_host_side_validation_without_gpu(lib):
                                None, 0, None) == _lib.DFMI_OK
     assert lib.dfmi_gather_qmm_affine(None, _lib.DFMI_BF16, 4, None, None, None, None, None, None,
                                       8, 256, 64, 4, 64, 8, None) == _lib.DFMI_EINVAL
-    assert lib.dfmi_moe_combine(None, _lib.DFMI_F32, None, None, 4, 2, 8, None) == _lib.DFMI_EINVAL
+    assert lib.dfmi_moe_combine(None, _lib.DFMI_F32, None, None, None, 4, 2, 8, None) == _lib.DFMI_EINVAL
 
 
 def test_workspace_queries(lib):

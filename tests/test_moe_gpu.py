@@ -169,3 +169,36 @@ def test_moe_combine(dev, T, k, D):
     diff = np.abs(got.astype(np.int32) - want.astype(np.int32))
     assert diff.max() <= 1
     assert (diff == 0).mean() > 0.99
+
+
+@pytest.mark.parametrize("T,k,D", [(16, 8, 2048), (3, 2, 100)])
+def test_moe_combine_unsort(dev, T, k, D):
+    """y handed over in a permuted (expert-sorted) order with y_rows = the
+    inverse permutation gives the same bits as the combine over y in pair
+    order; a row id out of range makes only its token's output NaN."""
+    import torch
+
+    from dflash_mlx_amd.moe import moe_combine
+
+    rng = np.random.default_rng(100 + T * k + D)
+    y = oracle.round_to_dtype(rng.standard_normal((T * k, D)).astype(np.float32), "bf16")
+    sc = rng.random((T, k)).astype(np.float32)
+    sc /= sc.sum(axis=1, keepdims=True)
+    order = rng.permutation(T * k)
+    inv = np.empty_like(order)
+    inv[order] = np.arange(T * k)
+    want = omoe.moe_combine(y, sc, dtype="bf16", out_dtype="bf16")
+    scd = torch.tensor(sc, device=dev)
+    plain = from_dev(moe_combine(to_dev(y, "bf16", dev), scd), "bf16")
+    y_sorted = to_dev(y[order], "bf16", dev)
+    rows = torch.tensor(inv, dtype=torch.int32, device=dev)
+    got = from_dev(moe_combine(y_sorted, scd, y_rows=rows), "bf16")
+    assert np.array_equal(got, plain)
+    diff = np.abs(got.astype(np.int32) - want.astype(np.int32))
+    assert diff.max() <= 1
+    bad = rows.clone()
+    bad[k * (T - 1)] = T * k  # first pair of the last token
+    out = oracle.to_f32(from_dev(moe_combine(y_sorted, scd, y_rows=bad), "bf16"), "bf16")
+    assert np.isnan(out[T - 1]).all()
+    assert np.array_equal(from_dev(moe_combine(y_sorted, scd, y_rows=bad), "bf16")[: T - 1],
+                          got[: T - 1])
