@@ -46,14 +46,22 @@ __device__ inline unsigned long long umax64(unsigned long long a, unsigned long 
   return a > b ? a : b;
 }
 
+// LDS scratch of greedy_publish_and_finish (the caller places it: a static
+// __shared__ object, or a slice of a kernel's dynamic LDS).
+struct GreedyLds {
+  int last;
+  int sink;
+  uint32_t post[kMaxGreedyRows];
+};
+
 // Publish this workgroup's keys for rows [r0, r1) (s_best[m] in LDS) and, in
 // the last workgroup to arrive, turn the keys into tokens, accept and bonus.
 __device__ inline void greedy_publish_and_finish(const GreedyOut& o,
                                                  const unsigned long long* s_best, int r0,
-                                                 int r1, unsigned total_blocks) {
-  __shared__ int s_last;
-  __shared__ uint32_t s_post[kMaxGreedyRows];
-  __shared__ int s_sink;
+                                                 int r1, unsigned total_blocks, GreedyLds* g) {
+  int& s_last = g->last;
+  int& s_sink = g->sink;
+  uint32_t* s_post = g->post;
   const int tid = threadIdx.x;
   if (tid >= r0 && tid < r1) {
     const unsigned long long old = __hip_atomic_fetch_max(
@@ -172,16 +180,22 @@ __global__ __launch_bounds__(kMaxWaves * 64) void lmhead_greedy_kernel(LmArgs a)
     }
   });
   __syncthreads();
-  greedy_publish_and_finish(a.out, s_best, 0, a.M, (unsigned)a.n_blocks);
+  __shared__ GreedyLds s_g;
+  greedy_publish_and_finish(a.out, s_best, 0, a.M, (unsigned)a.n_blocks, &s_g);
 }
 
 template <typename Tag, int GS, int MT, int WV>
 __global__ __launch_bounds__(64 * WV) void lmhead_stream_kernel(LmArgs a) {
   using S = Stream<Tag, GS, MT, WV>;
   constexpr int kThreads = 64 * WV;
-  __shared__ unsigned long long s_best[16 * MT];
+  // Dynamic LDS only (two workgroups of 4 wavefronts fill a CU's LDS): the
+  // epilogue's argmax keys and greedy scratch follow the reduction buffer.
+  static_assert(WV * S::RED_FLOATS * 4 + 16 * MT * 8 + sizeof(GreedyLds) <= S::LDS_BYTES,
+                "epilogue LDS");
+  unsigned long long* s_best =
+      reinterpret_cast<unsigned long long*>(dfmi_smem + WV * S::RED_FLOATS * 4);
+  GreedyLds* s_g = reinterpret_cast<GreedyLds*>(s_best + 16 * MT);
   const int tid = threadIdx.x;
-  if (tid < 16 * MT) s_best[tid] = 0ull;
   typename S::Ctx cx;
   cx.x = buffer_rsrc(a.h, (uint32_t)a.M * (uint32_t)a.K * 2u);
   cx.w = buffer_rsrc(a.w, (uint32_t)a.V * (uint32_t)(a.K / 2));
@@ -215,6 +229,7 @@ __global__ __launch_bounds__(64 * WV) void lmhead_stream_kernel(LmArgs a) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) mine[((t * MT + mt) * 4 + j) * 64 + cx.lane] = acc[t][mt][j];
   }
+  if (tid < 16 * MT) s_best[tid] = 0ull;
   __syncthreads();
   const float capr = a.softcap > 0.f ? round_t<Tag>(a.softcap) : 0.f;
   const float neg = round_t<Tag>(-1e9f);
@@ -233,7 +248,7 @@ __global__ __launch_bounds__(64 * WV) void lmhead_stream_kernel(LmArgs a) {
     }
   }
   __syncthreads();
-  greedy_publish_and_finish(a.out, s_best, 0, a.M, (unsigned)a.n_blocks);
+  greedy_publish_and_finish(a.out, s_best, 0, a.M, (unsigned)a.n_blocks, s_g);
 }
 
 struct GreedyArgs {
@@ -273,7 +288,8 @@ __global__ __launch_bounds__(kGreedyThreads) void greedy_kernel(GreedyArgs a) {
   for (int d = 1; d < 64; d <<= 1) best = umax64(best, __shfl_xor(best, d, 64));
   if ((tid & 63) == 0) atomicMax(&s_best[m], best);
   __syncthreads();
-  greedy_publish_and_finish(a.out, s_best, m, m + 1, gridDim.x * gridDim.y);
+  __shared__ GreedyLds s_g;
+  greedy_publish_and_finish(a.out, s_best, m, m + 1, gridDim.x * gridDim.y, &s_g);
 }
 
 __global__ void accept_kernel(const uint32_t* drafted, const uint32_t* posterior, int64_t L,
@@ -444,7 +460,8 @@ extern "C" int dfmi_lmhead_greedy_accept(const void* h, int h_dtype, const uint3
   const bool kfull = (K % kChunkK) == 0;
   const int mt = M <= 16 ? 1 : 2;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (stream_eligible(M, K, V, group_size)) {
+  // the streaming loop takes the whole K range in one scale / bias window
+  if (stream_eligible(M, K, V, group_size) && K / group_size <= sb_max_groups(kSbPieces)) {
     if (h_dtype == DFMI_BF16) launch_lm_stream<BF16>(group_size, mt, a.n_blocks, st, a);
     else launch_lm_stream<F16>(group_size, mt, a.n_blocks, st, a);
     return check_launch("dfmi_lmhead_greedy_accept");

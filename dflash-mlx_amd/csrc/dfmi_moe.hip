@@ -141,9 +141,9 @@ __global__ __launch_bounds__(kMaxWaves * 64) void gather_kernel(GatherArgs a) {
   }
 }
 
-template <typename Tag, int GS, bool GLU>
+template <typename Tag, int GS, bool GLU, int SBPC>
 __global__ __launch_bounds__(256) void gather_stream_kernel(GatherArgs a) {
-  using S = Stream<Tag, GS, 1, 4>;
+  using S = Stream<Tag, GS, 1, 4, SBPC>;
   constexpr int OUTC = GLU ? S::NB / 2 : S::NB;  // output columns per workgroup
   __shared__ int32_t s_rows[16];   // activation row of each MFMA row (clamped)
   __shared__ int32_t s_lhs[16];    // raw lhs ids of the current 16 pairs
@@ -247,23 +247,33 @@ __global__ __launch_bounds__(256) void gather_stream_kernel(GatherArgs a) {
   }
 }
 
-template <typename Tag, int GS, bool GLU>
+template <typename Tag, int GS, bool GLU, int SBPC>
 static void launch_gather_stream_t(const GatherArgs& a, hipStream_t st) {
-  using S = Stream<Tag, GS, 1, 4>;
+  using S = Stream<Tag, GS, 1, 4, SBPC>;
   constexpr int OUTC = GLU ? S::NB / 2 : S::NB;
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&gather_stream_kernel<Tag, GS, GLU>),
+      reinterpret_cast<const void*>(&gather_stream_kernel<Tag, GS, GLU, SBPC>),
       hipFuncAttributeMaxDynamicSharedMemorySize, S::LDS_BYTES);
   (void)attr;
   const dim3 grid((unsigned)((a.N + OUTC - 1) / OUTC), (unsigned)a.P);
-  hipLaunchKernelGGL((gather_stream_kernel<Tag, GS, GLU>), grid, dim3(256), S::LDS_BYTES, st, a);
+  hipLaunchKernelGGL((gather_stream_kernel<Tag, GS, GLU, SBPC>), grid, dim3(256), S::LDS_BYTES,
+                     st, a);
+}
+
+// The narrow scale window (8 pieces, 64 KB of LDS with 4 wavefronts) keeps
+// two workgroups per CU next to the kernel's static index arrays; K ranges
+// of more groups take the wide one (80 KB, one workgroup per CU).
+template <typename Tag, bool GLU, int GS>
+static void launch_gather_stream_gs(const GatherArgs& a, hipStream_t st) {
+  if (a.K / GS <= sb_max_groups(8)) launch_gather_stream_t<Tag, GS, GLU, 8>(a, st);
+  else launch_gather_stream_t<Tag, GS, GLU, kSbPieces>(a, st);
 }
 
 template <typename Tag, bool GLU>
 static void launch_gather_stream(const GatherArgs& a, int gs, hipStream_t st) {
-  if (gs == 32) launch_gather_stream_t<Tag, 32, GLU>(a, st);
-  else if (gs == 64) launch_gather_stream_t<Tag, 64, GLU>(a, st);
-  else launch_gather_stream_t<Tag, 128, GLU>(a, st);
+  if (gs == 32) launch_gather_stream_gs<Tag, GLU, 32>(a, st);
+  else if (gs == 64) launch_gather_stream_gs<Tag, GLU, 64>(a, st);
+  else launch_gather_stream_gs<Tag, GLU, 128>(a, st);
 }
 
 template <typename Tag, int GS, int NT, bool KFULL, bool GLU>
@@ -355,12 +365,14 @@ static int gather_common(const void* x, int x_dtype, int64_t x_rows, const uint3
   a.E = (int)E;
   a.chunks = (int)((K + kChunkK - 1) / kChunkK);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  // streaming loop: whole 256-k steps and scale blocks, 32-bit buffer offsets
-  // per expert and for the activations.  Measured on MI355X (16 tokens, top-8
-  // of 256 experts): equal to the general loop for the SwiGLU pair at K = 2048
-  // and slower for K = 512 (two steps per workgroup do not amortise its
-  // pipeline fill), so short K stays on the general loop.
-  if (stream_eligible(16, K, N, group_size) && K >= 1024 && x_rows * K * 2 < (1ll << 31)) {
+  // streaming loop: whole 256-k steps, the whole K in one scale / bias
+  // window, 32-bit buffer offsets per expert and for the activations.
+  // Measured on MI355X (16 tokens, top-8 of 256 experts): equal to the
+  // general loop for the SwiGLU pair at K = 2048 and slower for K = 512 (two
+  // steps per workgroup do not amortise its pipeline fill), so short K stays
+  // on the general loop.
+  if (stream_eligible(16, K, N, group_size) && K >= 1024 && x_rows * K * 2 < (1ll << 31) &&
+      K / group_size <= sb_max_groups(kSbPieces)) {
     if (glu) {
       if (x_dtype == DFMI_BF16) launch_gather_stream<BF16, true>(a, group_size, st);
       else launch_gather_stream<F16, true>(a, group_size, st);

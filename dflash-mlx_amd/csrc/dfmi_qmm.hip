@@ -301,7 +301,6 @@ static int stream_waves(int64_t M, int64_t K, int grid) {
 
 static int plan_stream(int64_t M, int64_t K, int64_t N, int gs, const dfmi_qmm_tuning* tune,
                        StreamPlan& p) {
-  (void)gs;
   p.MT = M <= 16 ? 1 : 2;
   p.n_blocks = (int)((N + kStreamRows - 1) / kStreamRows);
   int kp;
@@ -321,6 +320,9 @@ static int plan_stream(int64_t M, int64_t K, int64_t N, int gs, const dfmi_qmm_t
     p.WV = tune->waves_per_block;
   p.chunks = (int)(K / (64 * p.WV));
   p.kp = std::min(p.kp, p.chunks);
+  // a split's K range fits one scale / bias window
+  const int max_chunks = sb_max_groups(kSbPieces) / (64 * p.WV / gs);
+  p.kp = std::max(p.kp, (p.chunks + max_chunks - 1) / max_chunks);
   p.xcd_map = (p.n_blocks % 8 == 0) ? 1 : 0;
   p.grid_x = p.n_blocks * p.kp;
   p.ws_bytes = p.kp > 1 ? kCounterBytes + (size_t)p.kp * (size_t)M * (size_t)N * 4u : 0;
@@ -535,7 +537,9 @@ static bool use_stream(int64_t M, int64_t K, int64_t N, int gs, int bits,
   const int path = tune ? tune->path : 0;
   if (bits != 4) return false;
   if (path == 1 || path == 3) return false;
-  return stream_eligible(M, K, N, gs);
+  // more blocks than split counters run unsplit: the whole K in one scale window
+  return stream_eligible(M, K, N, gs) &&
+         ((N + kStreamRows - 1) / kStreamRows <= kMaxCounters || K / gs <= sb_max_groups(kSbPieces));
 }
 
 extern "C" size_t dfmi_qmm_workspace_bytes_ex(int64_t M, int64_t K, int64_t N, int group_size,

@@ -7,9 +7,10 @@
 //   * a CU's vector memory pipeline retires roughly one cache-line request
 //     every few cycles however few bytes of the line an instruction uses, so
 //     every global read is a whole-line request: weights (whole 32*WV-byte
-//     row pieces), activations (whole rows) and scales / biases (8 rows x
-//     64 B of each array) go straight to LDS with buffer_load ... lds,
-//     DEPTH - 1 steps ahead;
+//     row pieces), activations (whole rows) and scales / biases (each row's
+//     window for the whole K range, contiguous across rows when the range is
+//     all of K) go straight to LDS with buffer_load ... lds, the steps
+//     DEPTH - 1 ahead and the scales / biases once before the first step;
 //   * the loop is VALU-issue bound (a SIMD retires one wave64 VALU op per
 //     ~4.2 cycles), so every address is computed once per lane: a DMA is an
 //     SGPR base (advanced by scalar adds) plus a lane-constant VGPR offset,
@@ -47,7 +48,13 @@ namespace dfmi {
 
 constexpr int kStreamRows = 64;   // weight rows per workgroup
 constexpr int kStreamTiles = 4;   // 16-row MFMA tiles per workgroup, all in every wavefront
-constexpr uint32_t kNoRow = 0x80000000u;  // buffer offset of an activation row past M
+constexpr uint32_t kNoRow = 0x80000000u;  // buffer offset past the end of every buffer
+// Scale / bias window of a run() call: at most SBPC 16-byte pieces (8
+// groups each) per row and array, so a K range of at most sb_max_groups(SBPC)
+// quantisation groups whatever its first group (a window may start
+// mid-piece).
+constexpr int kSbPieces = 16;
+constexpr int sb_max_groups(int sbpc) { return 8 * (sbpc - 1); }
 
 // Wait until at most N vector-memory operations of this wavefront are
 // outstanding and all LDS operations are done, then the workgroup barrier.
@@ -86,37 +93,39 @@ __device__ inline uint32_t opaque(uint32_t v) {
   return v;
 }
 
-template <typename Tag, int GS, int MT, int WV>
+template <typename Tag, int GS, int MT, int WV, int SBPC = kSbPieces>
 struct Stream {
   static constexpr int NT = kStreamTiles;
   static constexpr int NB = kStreamRows;
   static constexpr int CK = 64 * WV;        // k per step
   static constexpr int GPC = CK / GS;       // quantisation groups per step
-  static constexpr int SBC = 32 / GPC;      // steps per scale / bias block (32 groups)
   static constexpr int XROW = CK * 2;       // bytes of one activation row per step
   static constexpr int XPPR = CK / 8;       // 16-byte pieces per activation row
   static constexpr int WROW = CK / 2;       // bytes of one weight row per step
   static constexpr int WPPR = WROW / 16;    // 16-byte pieces per weight row
   static_assert(WV == 4 || WV == 8, "wavefronts");
-  static_assert(SBC >= 2, "scale block reuse distance");
-  // LDS stages (DEPTH - 1 steps in flight).  A scale block's buffer is
-  // rewritten DEPTH - 1 steps ahead of its last reader, so SBC >= DEPTH - 1
-  // keeps the two scale buffers apart.  Four stages with 8 wavefronts
-  // (144 KB of LDS) measured slower than three on MI355X (4096x12288:
-  // 12.8 us vs 11.4 us): the extra step in flight does not raise the per-CU
-  // request rate, and the longer wait chain delays the first MFMA.
+  // LDS stages (DEPTH - 1 steps in flight).  Four stages with 8 wavefronts
+  // measured slower than three on MI355X (4096x12288: 12.8 us vs 11.4 us):
+  // the extra step in flight does not raise the per-CU request rate, and the
+  // longer wait chain delays the first MFMA.
   static constexpr int DEPTH = 3;
-  static_assert(SBC >= DEPTH - 1, "scale buffers");
   // gs >= 64: a lane's two k-blocks take adjacent words (one 8-byte LDS read);
   // gs = 32: k-block j is group 2*wave + j, so the blocks stay group-pure.
   static constexpr bool PAIR = GS >= 64;
   static constexpr int XBUF = MT * 16 * XROW;  // bytes of one activation stage
   static constexpr int WBUF = NB * WROW;       // bytes of one weight stage
-  static constexpr int SBBUF = NB * 128;       // 64 B of scales per row, then 64 B of biases per row
-  // Scale / bias buffers first: their fragment reads use immediate offsets
+  // Scales and biases of the whole K range of a run() call, loaded once
+  // before its first step: [array][row][SBP bytes], a row's window of 16-byte
+  // pieces (8 groups each) XOR-swizzled by row.  Up to SBPC pieces, i.e. a
+  // K range of at most MAX_GROUPS groups (any start).
+  static_assert(SBPC == 8 || SBPC == 16, "scale window pieces");
+  static constexpr int MAX_GROUPS = sb_max_groups(SBPC);
+  static constexpr int SBP = 16 * SBPC;        // bytes per row and array
+  static constexpr int SBBUF = 2 * NB * SBP;   // scales, then biases
+  // Scale / bias region first: its fragment reads use immediate offsets
   // (the ds_read offset field is 16 bits).
   static constexpr int SB_OFF = 0;
-  static constexpr int X_OFF = 2 * SBBUF;
+  static constexpr int X_OFF = SBBUF;
   static constexpr int W_OFF = X_OFF + DEPTH * XBUF;
   static constexpr int LDS_BYTES = W_OFF + DEPTH * WBUF;
   static_assert(LDS_BYTES <= 160 * 1024, "LDS");
@@ -126,7 +135,8 @@ struct Stream {
   // DMA instructions (1 KiB each) per wavefront
   static constexpr int X_DMA = XBUF / 1024 / WV;    // = 2 * MT
   static constexpr int W_DMA = WBUF / 1024 / WV;    // = 2
-  static constexpr int SB_DMA = SBBUF / 1024 / WV;  // 2 (WV = 4) or 1 (WV = 8)
+  static constexpr int SB_DMA = SBBUF / 1024 / WV;  // 2 SBPC / WV, once per run()
+  static constexpr int SB_RPI = 1024 / SBP;         // rows per scale / bias instruction
   static constexpr int CHUNK_DMA = X_DMA + W_DMA;
   static_assert(GS == 32 || GS == 64 || GS == 128, "group size");
 
@@ -160,7 +170,8 @@ struct Stream {
     uint32_t wg[W_DMA];  // weight DMA: byte offset in w at step 0
     uint32_t xo[2];      // activation fragment j: byte offset inside a stage (M-block 0)
     uint32_t wo[2];      // weight fragment (j = 0; j = 1 too at gs = 32): offset inside a stage (tile 0)
-    uint32_t sbl;        // scale fragment: row offset with its swizzle bits (tile 0, buffer 0)
+    uint32_t sbr;        // scale fragment: row offset (tile 0)
+    uint32_t swz;        // scale window swizzle key of this lane's row: col % SBPC
     uint32_t hsel;       // v_perm selector moving this wavefront's 16-bit half to the high half
   };
 
@@ -214,7 +225,8 @@ struct Stream {
       const int byte = piece_of(cx.wave, kg, j) * 4;
       L.wo[j] = (uint32_t)(col * WROW + (((byte >> 4) ^ (col % WPPR)) * 16) + (byte & 15));
     }
-    L.sbl = (uint32_t)(col * 64 + (((col >> 2) & 3) << 4));
+    L.sbr = (uint32_t)(col * SBP);
+    L.swz = (uint32_t)(col % SBPC);
     const int half = PAIR ? (((cx.wave * 64) / GS) & 1) : 0;
     L.hsel = half ? 0x03020c0cu : 0x01000c0cu;
     return L;
@@ -238,27 +250,28 @@ struct Stream {
     }
   }
 
-  // Scale / bias block sb = groups [32 sb, 32 sb + 32) of every row, laid
-  // out as [array][row][64 B] (4 pieces of 16 B per row and array).
-  // Instruction j of the workgroup (array j / 4, rows 16 (j % 4) .. +15):
-  // lane l loads piece (l & 3) ^ ((row >> 2) & 3) of row r0 + (l >> 2) into
-  // slot l & 3.  Pieces past the end of a row re-read its last piece (never
-  // used).  Once per SBC steps, so its addresses are computed here.
-  __device__ static inline void issue_sb(const Ctx& cx, int sb, int buf) {
-    const int last_piece = cx.groups / 8 - 1;  // 8 16-bit values per piece
+  // Scale / bias window: pieces [piece0, piece0 + P) (8 groups each) of
+  // every row and array.  Instruction j of the workgroup covers array
+  // j / (NB / SB_RPI), rows r0 .. r0 + SB_RPI - 1; lane l takes slot
+  // l % SBPC of row r0 + l / SBPC, which holds piece
+  // piece0 + (slot ^ (row % SBPC)).  Slots past the window, and rows past N,
+  // read past the end of the buffer (zeros, no memory request).
+  __device__ static inline void issue_sb(const Ctx& cx, int piece0, int P) {
 #pragma unroll
     for (int i = 0; i < SB_DMA; ++i) {
-      const int j = cx.wave * SB_DMA + i;  // 0 .. 7, wave-uniform
-      const int arr = j >> 2;
-      const int r0 = (j & 3) * 16;
-      const int r = r0 + (cx.lane >> 2);
-      const int q = (cx.lane & 3) ^ ((r >> 2) & 3);
-      const bool second = r0 >= cx.split;  // wave-uniform
-      const int n = min(cx.n0 + (second ? r - cx.split : r), cx.N - 1);
-      const int piece = min(sb * 4 + q, last_piece);
-      const uint32_t off = ((uint32_t)n * (uint32_t)cx.groups + (uint32_t)piece * 8u) * 2u;
+      const int j = cx.wave * SB_DMA + i;  // wave-uniform
+      const int arr = j / (NB / SB_RPI);
+      const int r0 = (j % (NB / SB_RPI)) * SB_RPI;
+      const int r = r0 + cx.lane / SBPC;
+      const int q = (cx.lane % SBPC) ^ (r % SBPC);
+      const bool second = r0 >= cx.split;  // wave-uniform (split is a multiple of SB_RPI)
+      const int n = cx.n0 + (second ? r - cx.split : r);
+      const uint32_t off =
+          (q < P && n < cx.N)
+              ? ((uint32_t)n * (uint32_t)cx.groups + (uint32_t)(piece0 + q) * 8u) * 2u
+              : kNoRow;
       const __amdgpu_buffer_rsrc_t src = arr ? (second ? cx.b2 : cx.b) : (second ? cx.s2 : cx.s);
-      dma16(src, off, 0u, dfmi_smem + SB_OFF + buf * SBBUF + arr * 4096 + r0 * 64);
+      dma16(src, off, 0u, dfmi_smem + SB_OFF + arr * NB * SBP + r0 * SBP);
     }
   }
 
@@ -267,8 +280,9 @@ struct Stream {
     issue_w(cx, L, c, stage);
   }
 
-  // Step c's fragments of this lane from LDS stage `stage`, scale buffer sbuf.
-  __device__ static inline void read_frag(const Ctx& cx, const Lane& L, int c, int stage, int sbuf,
+  // Step c's fragments of this lane from LDS stage `stage`; g0w = first
+  // group of the scale window (a multiple of 8).
+  __device__ static inline void read_frag(const Ctx& cx, const Lane& L, int c, int stage, int g0w,
                                           Frag& f) {
     const uint32_t xb = opaque((uint32_t)(X_OFF + stage * XBUF));
     const uint32_t wb = opaque((uint32_t)(W_OFF + stage * WBUF));
@@ -281,11 +295,12 @@ struct Stream {
     }
     const char* ws0 = dfmi_smem + (L.wo[0] + wb);
     const char* ws1 = dfmi_smem + (L.wo[1] + wb);
-    // this step's group inside the scale block: byte offset gi*2 of the row's
-    // 64-byte block, as 16-byte piece (swizzled by XOR) and dword offset
-    const int gi = (c % SBC) * GPC + (PAIR ? (cx.wave * 64) / GS : 2 * cx.wave);
-    const uint32_t u = (uint32_t)(sbuf * SBBUF + gi * 2) & ~3u;
-    const char* sbp = dfmi_smem + SB_OFF + (L.sbl ^ u);
+    // this step's group in the window: piece gr / 8 (stored at slot
+    // (gr / 8) ^ (col % SBPC)), dword (gr % 8) / 2 of the piece
+    const uint32_t gr =
+        (uint32_t)(c * GPC + (PAIR ? (cx.wave * 64) / GS : 2 * cx.wave) - g0w);
+    const char* sbp =
+        dfmi_smem + SB_OFF + (L.sbr + (((gr >> 3) ^ L.swz) << 4) + ((gr & 7) >> 1) * 4);
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       if constexpr (PAIR) {
@@ -296,8 +311,8 @@ struct Stream {
         f.w[t][0] = *reinterpret_cast<const uint32_t*>(ws0 + t * 16 * WROW);
         f.w[t][1] = *reinterpret_cast<const uint32_t*>(ws1 + t * 16 * WROW);
       }
-      f.sv[t] = *reinterpret_cast<const uint32_t*>(sbp + t * 16 * 64);
-      f.bv[t] = *reinterpret_cast<const uint32_t*>(sbp + t * 16 * 64 + 4096);
+      f.sv[t] = *reinterpret_cast<const uint32_t*>(sbp + t * 16 * SBP);
+      f.bv[t] = *reinterpret_cast<const uint32_t*>(sbp + t * 16 * SBP + NB * SBP);
     }
   }
 
@@ -362,8 +377,8 @@ struct Stream {
   }
 
   // Barrier once this wavefront has at most n whole steps of loads
-  // outstanding (n <= 3).  A scale block issued with one of those steps (it
-  // precedes their activations and weights) is over-waited: it lands with them.
+  // outstanding (n <= 3).  The scale window precedes every step's loads, so
+  // it has landed by the first wait.
   __device__ static inline void wait_steps(int n) {
     if (n >= 3) stage_barrier<3 * CHUNK_DMA>();
     else if (n == 2) stage_barrier<2 * CHUNK_DMA>();
@@ -374,47 +389,43 @@ struct Stream {
   // iteration c: step c+1 must be in LDS (steps c+2 .. c+DEPTH-1 may still
   // be in flight); step c is in `cur`.
   __device__ static inline void step(const Ctx& cx, const Lane& L, int c, int c1, int stage,
-                                     Frag& cur, Frag& nxt, f32x4 (&acc)[NT][MT],
+                                     int g0w, Frag& cur, Frag& nxt, f32x4 (&acc)[NT][MT],
                                      const DqConst& dq) {
     if (c + 1 < c1) {
       wait_steps(min(DEPTH - 2, c1 - c - 2));
-      if (c + DEPTH < c1) {
-        if ((c + DEPTH) % SBC == 0) issue_sb(cx, (c + DEPTH) / SBC, ((c + DEPTH) / SBC) & 1);
+      if (c + DEPTH < c1)
         issue_chunk(cx, L, c + DEPTH, stage);  // step c's stage: its fragments are in cur
-      }
       const int st1 = stage == DEPTH - 1 ? 0 : stage + 1;
-      read_frag(cx, L, c + 1, st1, ((c + 1) / SBC) & 1, nxt);
+      read_frag(cx, L, c + 1, st1, g0w, nxt);
     }
     compute(L, cur, acc, dq);
   }
 
   // Accumulate steps [c0, c1) (c1 > c0) of this workgroup into acc.  Every
   // wavefront of the workgroup calls this with the same range (it contains
-  // barriers).
+  // barriers).  The range covers at most MAX_GROUPS groups.
   __device__ static inline void run(const Ctx& cx, int c0, int c1, f32x4 (&acc)[NT][MT]) {
     const DqConst dq = dq_const<Tag>();
     const Lane L = lane_setup(cx);
-    issue_sb(cx, c0 / SBC, (c0 / SBC) & 1);
+    const int piece0 = (c0 * GPC) >> 3;
+    const int g0w = piece0 * 8;
+    issue_sb(cx, piece0, ((c1 * GPC + 7) >> 3) - piece0);
     issue_chunk(cx, L, c0, 0);
 #pragma unroll
-    for (int k = 1; k < DEPTH; ++k) {
-      if (c0 + k < c1) {
-        if ((c0 + k) % SBC == 0) issue_sb(cx, (c0 + k) / SBC, ((c0 + k) / SBC) & 1);
-        issue_chunk(cx, L, c0 + k, k);
-      }
-    }
+    for (int k = 1; k < DEPTH; ++k)
+      if (c0 + k < c1) issue_chunk(cx, L, c0 + k, k);
     // step c0 in LDS: at most the loads of steps c0+1 .. c0+DEPTH-1 outstanding
     wait_steps(min(DEPTH - 1, c1 - c0 - 1));
     Frag fa, fb;
-    read_frag(cx, L, c0, 0, (c0 / SBC) & 1, fa);
+    read_frag(cx, L, c0, 0, g0w, fa);
     int c = c0, stage = 0;
     for (; c + 1 < c1; c += 2) {
-      step(cx, L, c, c1, stage, fa, fb, acc, dq);
+      step(cx, L, c, c1, stage, g0w, fa, fb, acc, dq);
       stage = stage == DEPTH - 1 ? 0 : stage + 1;
-      step(cx, L, c + 1, c1, stage, fb, fa, acc, dq);
+      step(cx, L, c + 1, c1, stage, g0w, fb, fa, acc, dq);
       stage = stage == DEPTH - 1 ? 0 : stage + 1;
     }
-    if (c < c1) step(cx, L, c, c1, stage, fa, fb, acc, dq);
+    if (c < c1) step(cx, L, c, c1, stage, g0w, fa, fb, acc, dq);
   }
 };
 
