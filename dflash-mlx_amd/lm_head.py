@@ -86,6 +86,27 @@ def lm_head_greedy_accept(h: torch.Tensor, w: torch.Tensor, scales: torch.Tensor
     return GreedyAcceptResult(posterior, accept, bonus, logits)
 
 
+def draft_tokens_from_hidden(draft_hidden: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
+                             biases: torch.Tensor, *,
+                             suppress_token_mask: Optional[torch.Tensor] = None,
+                             softcap: Optional[float] = None, group_size: int = 64,
+                             bits: int = 4) -> torch.Tensor:
+    """Draft block tokens from the draft model's hidden states.
+
+    dflash_mlx/draft_backend.py:142-149: the target's lm_head over
+    ``draft_hidden[:, 1:, :]`` (block_len - 1 rows, e.g. 15) followed by
+    ``greedy_tokens_with_mask(...).squeeze(0)``.  One fused kernel: the
+    lm_head epilogue reduces to the per-row argmax, no logits are written
+    and no accept step runs.  ``draft_hidden`` is ``[1, block_len, K]``
+    (or ``[block_len, K]``); returns int32 ``[block_len - 1]``."""
+    h = draft_hidden[0] if draft_hidden.dim() == 3 else draft_hidden
+    if h.dim() != 2 or int(h.shape[0]) < 2:
+        raise ValueError("draft_hidden must be [1, block_len, K] with block_len > 1")
+    res = lm_head_greedy_accept(h[1:], w, scales, biases, suppress_token_mask=suppress_token_mask,
+                                softcap=softcap, group_size=group_size, bits=bits)
+    return res.posterior
+
+
 def greedy_accept(logits: torch.Tensor, *, verify_ids: Optional[torch.Tensor] = None,
                   suppress_token_mask: Optional[torch.Tensor] = None) -> GreedyAcceptResult:
     """Greedy + accept/bonus over ``logits [..., V]`` (at most 32 rows)."""

@@ -211,3 +211,39 @@ def test_lmhead_repeatable_and_workspace_clean(dev):
                               oracle.greedy_tokens_with_mask(lg, dtype="bf16"))
         again = lm_head_greedy_accept(*args, group_size=gs, bits=4).posterior.cpu().numpy()
         assert np.array_equal(again, first)
+
+
+@pytest.mark.parametrize("block_len,K,V,gs", [(16, 2048, 32000, 64), (16, 1024, 5003, 32),
+                                              (8, 5120, 20000, 64)])
+def test_draft_tokens_from_hidden(dev, block_len, K, V, gs):
+    """Draft side (dflash_mlx/draft_backend.py:142-149): the target lm_head
+    over draft_hidden[:, 1:, :] (block_len - 1 rows, e.g. 15) and the masked
+    greedy argmax, fused, no accept.  Tokens equal the greedy argmax of the
+    kernel's own logits (which are within the parity metric of the oracle),
+    with and without a suppress mask."""
+    import torch
+
+    from dflash_mlx_amd.lm_head import draft_tokens_from_hidden, lm_head_greedy_accept
+    from dflash_mlx_amd.sampling import build_suppress_token_mask
+
+    M = block_len - 1
+    x, w_q, s, b = _lm_case(block_len, K, V, gs, seed=block_len + K + V)
+    hd = to_dev(x, "bf16", dev).reshape(1, block_len, K)
+    wd, sd, bd = to_dev(w_q, "u32", dev), to_dev(s, "bf16", dev), to_dev(b, "bf16", dev)
+    full = lm_head_greedy_accept(hd[0, 1:], wd, sd, bd, group_size=gs, return_logits=True)
+    got_logits = from_dev(full.logits, "bf16")
+    exact = oracle.quantized_matmul(x[1:], w_q, s, b, group_size=gs, dtype="bf16")
+    _, rel = oracle.parity_metrics(oracle.to_f32(got_logits, "bf16"), exact)
+    assert rel <= 1e-2
+    toks = draft_tokens_from_hidden(hd, wd, sd, bd, group_size=gs)
+    assert toks.shape == (M,)
+    assert np.array_equal(toks.cpu().numpy(), oracle.greedy_tokens_with_mask(got_logits, dtype="bf16"))
+    # suppress the current winners of the first rows: the next best take over
+    banned = sorted(set(int(t) for t in toks.cpu().numpy()[:3]))
+    mask = build_suppress_token_mask(V, banned, device=dev)
+    toks_m = draft_tokens_from_hidden(hd, wd, sd, bd, suppress_token_mask=mask, group_size=gs)
+    mask_np = np.zeros(V, bool)
+    mask_np[banned] = True
+    want = oracle.greedy_tokens_with_mask(got_logits, mask_np, dtype="bf16")
+    assert np.array_equal(toks_m.cpu().numpy(), want)
+    assert not np.isin(toks_m.cpu().numpy(), banned).any()
