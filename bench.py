@@ -21,9 +21,10 @@ host's cores, on a bounded sample: layer 0's seven matmuls).
 Other workloads (``--workload``, not the default line): ``27b`` (64 layers,
 hidden 5120, ``--m`` 8/16/32), ``single`` ([16,4096]x[4096,4096], weights
 rotated over a 1 GB pool), ``lmhead`` (fused lm_head [16,5120]x[151936,5120]
-+ greedy accept) and ``moe`` (40 layers of top-8-of-256 routed experts,
-hidden 2048, expert width 512).  ``copy`` is a 512 MiB device copy used to
-calibrate the HBM traffic counters.
++ greedy accept), ``moe`` (40 layers of top-8-of-256 routed experts,
+hidden 2048, expert width 512) and ``gdn`` (the GDN rollback pair of a verify
+cycle: gated delta + tape over 16 steps, replay of 9, per layer).  ``copy``
+is a 512 MiB device copy used to calibrate the HBM traffic counters.
 """
 
 from __future__ import annotations
@@ -405,6 +406,55 @@ def run_moe(args, torch):
     return base_result(args, gbs, ms, 3 * layers, config, roofline)
 
 
+def run_gdn(args, torch):
+    """GDN rollback pair of one verify cycle per GDN layer: the recurrence with
+    tape over the 16-token block, then the replay of 9 accepted steps, on 64
+    layers' worth of distinct fp32 states (the state, 4 MiB per layer, is the
+    traffic that bounds both kernels)."""
+    from dflash_mlx_amd.gdn import gated_delta_kernel_with_tape, tape_replay_kernel
+
+    dev = torch.device("cuda:0")
+    B, T, Hk, Hv, Dk, Dv, layers, acc = 1, 16, 16, 32, 128, 128, 64, 8
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(11)
+    q = (torch.randn((B, T, Hk, Dk), generator=gen, device=dev) / Dk ** 0.5).to(torch.bfloat16)
+    k = (torch.randn((B, T, Hk, Dk), generator=gen, device=dev) / Dk ** 0.5).to(torch.bfloat16)
+    v = torch.randn((B, T, Hv, Dv), generator=gen, device=dev).to(torch.bfloat16)
+    g = torch.rand((B, T, Hv), generator=gen, device=dev) * 0.15 + 0.85
+    beta = torch.rand((B, T, Hv), generator=gen, device=dev).to(torch.bfloat16)
+    states = [torch.randn((B, Hv, Dv, Dk), generator=gen, device=dev) * 0.1 for _ in range(layers)]
+    tapes = [gated_delta_kernel_with_tape(q, k, v, g, beta, s_)[2] for s_ in states]
+
+    def fn_tape():
+        for s_ in states:
+            gated_delta_kernel_with_tape(q, k, v, g, beta, s_)
+
+    def fn_replay():
+        for s_, t_ in zip(states, tapes):
+            tape_replay_kernel(t_[:, :acc + 1], k[:, :acc + 1], g[:, :acc + 1], s_)
+
+    ms_tape = time_replays(torch, graph_of(torch, fn_tape), args.steps, warmup=args.warmup)
+    ms_rep = time_replays(torch, graph_of(torch, fn_replay), args.steps, warmup=args.warmup)
+    st_bytes = B * Hv * Dv * Dk * 4
+    tape_bytes = 2 * st_bytes + 2 * B * T * Hk * Dk * 2 + 2 * B * T * Hv * Dv * 2 \
+        + B * T * Hv * Dv * 4 + B * T * Hv * 6
+    rep_bytes = 2 * st_bytes + (acc + 1) * (B * Hv * Dv * 4 + B * Hk * Dk * 2 + B * Hv * 4)
+    us_tape = ms_tape * 1e3 / layers
+    us_rep = ms_rep * 1e3 / layers
+    gbs = tape_bytes / (us_tape * 1e-6) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": "gdn_kernel<4, false>", "bytes_per_launch": tape_bytes,
+                "us_per_launch": round(us_tape, 3),
+                "replay": {"kernel": "gdn_kernel<4, true>", "steps": acc + 1,
+                           "bytes_per_launch": rep_bytes, "us_per_launch": round(us_rep, 3),
+                           "GBps": round(rep_bytes / (us_rep * 1e-6) / 1e9, 2)}}
+    config = {"workload": "GDN rollback pair per layer: gated delta + tape over 16 steps, "
+                          "replay of 9 steps; B=1, Hk=16, Hv=32, Dk=Dv=128, fp32 state, 64 layers",
+              "T": T, "Hk": Hk, "Hv": Hv, "Dk": Dk, "Dv": Dv}
+    return base_result(args, gbs, ms_tape, layers, config, roofline)
+
+
 def run_copy(args, torch):
     """Plain device copy of a known size: calibrates the FETCH_SIZE /
     WRITE_SIZE counters (bytes per dispatch read and written are both
@@ -434,7 +484,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="9b",
-                    choices=["9b", "27b", "single", "lmhead", "moe", "copy"])
+                    choices=["9b", "27b", "single", "lmhead", "moe", "gdn", "copy"])
     ap.add_argument("--m", type=int, default=16)
     ap.add_argument("--path", type=int, default=0, help="1 general kernel, 2 streaming kernel")
     ap.add_argument("--tiles", type=int, default=0)
@@ -452,7 +502,7 @@ def main():
 
     __graft_entry__.load_package()
     runner = {"9b": run_sweep, "27b": run_sweep, "single": run_single, "lmhead": run_lmhead,
-              "moe": run_moe, "copy": run_copy}[args.workload]
+              "moe": run_moe, "gdn": run_gdn, "copy": run_copy}[args.workload]
     res = runner(args, torch)
     print(json.dumps(res), flush=True)
 

@@ -192,6 +192,40 @@ int dfmi_lmhead_greedy_accept(const void *h, int h_dtype, const uint32_t *w_q, c
 size_t dfmi_lmhead_workspace_bytes(int64_t M);
 
 /*
+ * Gated-delta recurrence recording the innovation tape, over T steps
+ * (dflash_mlx/kernels.py:11-219 gated_delta_kernel_with_tape; called from
+ * dflash_mlx/engine/target_qwen_gdn.py:615-625 while the rollback cache is
+ * armed).  Per batch b, value head hv (key head hv / (Hv/Hk)), state row dv,
+ * unmasked step t:  S *= g;  d = (v[dv] - S.k) * beta;  S += d k;
+ * y[dv] = S.q;  tape[dv] = d  (masked steps: S kept, y = 0, tape = 0).
+ *   q, k [B, T, Hk, Dk], v / y [B, T, Hv, Dv] in qkv_dtype;
+ *   g [B, T, Hv] (g_per_key = 0) or [B, T, Hv, Dk] in g_dtype;
+ *   beta [B, T, Hv] in beta_dtype; mask uint8 [B, T] (nonzero = live) or NULL;
+ *   state_in / state_out [B, Hv, Dv, Dk] in state_dtype (may alias);
+ *   tape [B, T, Hv, Dv] fp32.
+ * The state is carried in fp32 across the steps.  Dk in {32, 64, 128, 256,
+ * 512}, Hv a multiple of Hk, B*Hv <= 65535.
+ */
+int dfmi_gated_delta_tape(const void *q, const void *k, const void *v, const void *g,
+                          const void *beta, const void *state_in, const uint8_t *mask, void *y,
+                          void *state_out, float *tape, int64_t B, int64_t T, int64_t Hk,
+                          int64_t Hv, int64_t Dk, int64_t Dv, int qkv_dtype, int g_dtype,
+                          int beta_dtype, int state_dtype, int g_per_key, void *stream);
+
+/*
+ * Tape replay over the accepted steps (dflash_mlx/kernels.py:691-866
+ * tape_replay_kernel; called by dflash_mlx/recurrent_rollback_cache.py:142-165
+ * with the first accepted+1 steps): per unmasked step
+ * S = round(S * g + tape[dv] * k) to state_dtype.
+ *   tape fp32 [B, T, Hv, Dv]; k [B, T, Hk, Dk] in k_dtype; g as above;
+ *   state_in / state_out [B, Hv, Dv, Dk] in state_dtype (may alias).
+ */
+int dfmi_tape_replay(const float *tape, const void *k, const void *g, const void *state_in,
+                     const uint8_t *mask, void *state_out, int64_t B, int64_t T, int64_t Hk,
+                     int64_t Hv, int64_t Dk, int64_t Dv, int k_dtype, int g_dtype,
+                     int state_dtype, int g_per_key, void *stream);
+
+/*
  * match_acceptance_length on device arrays (dflash_mlx/engine/acceptance.py:9-16):
  * out[0] = length of the longest prefix with drafted[i] == posterior[i]; 0 for L == 0.
  */

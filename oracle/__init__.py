@@ -38,6 +38,11 @@ Functions and what pins each one (see ``tests/test_oracle.py``):
   cycle, dflash_mlx/engine/spec_epoch.py:2011-2021, 2067-2072, 2129.
 * ``logit_softcap``              -- dflash_mlx/engine/target_gemma4.py:33-40,
   op-by-op rounding to the logits dtype (parity unpinned against MLX's tanh).
+* ``gated_delta_with_tape`` / ``tape_replay`` -- the GDN rollback pair,
+  dflash_mlx/kernels.py:11-219 and 691-866 (gdn.py).  Pinned by a brute-force
+  loop form, closed forms (beta = 0; one step from a zero state), masked
+  steps, and the rollback invariant: replaying the full tape reproduces the
+  recurrence's final state.
 
 bf16 tensors are carried as ``uint16`` bit patterns; fp16 as ``numpy.float16``.
 """
@@ -68,4 +73,9 @@ from .moe import (  # noqa: F401
     route_topk,
     switch_glu,
     moe_combine,
+)
+from .gdn import (  # noqa: F401
+    gated_delta_with_tape,
+    gated_delta_with_tape_loops,
+    tape_replay,
 )

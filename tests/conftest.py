@@ -62,6 +62,8 @@ def to_dev(a: np.ndarray, dtype: str, dev):
         return torch.from_numpy(a.astype(np.uint16).view(np.int16)).view(torch.bfloat16).to(dev)
     if dtype == "f16":
         return torch.from_numpy(a.astype(np.float16)).to(dev)
+    if dtype == "f32":
+        return torch.from_numpy(a.astype(np.float32)).to(dev)
     if dtype == "u32":
         return torch.from_numpy(a.astype(np.uint32).view(np.int32)).to(dev)
     if dtype == "i32":

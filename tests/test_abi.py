@@ -70,6 +70,18 @@ def test_host_side_validation_without_gpu(lib):
     assert lib.dfmi_gather_qmm_affine(None, _lib.DFMI_BF16, 4, None, None, None, None, None, None,
                                       8, 256, 64, 4, 64, 8, None) == _lib.DFMI_EINVAL
     assert lib.dfmi_moe_combine(None, _lib.DFMI_F32, None, None, None, 4, 2, 8, None) == _lib.DFMI_EINVAL
+    # GDN pair: Dk must be 32 * {1, 2, 4, 8, 16}, Hv a multiple of Hk, float dtypes
+    bf, f32 = _lib.DFMI_BF16, _lib.DFMI_F32
+    gdn = [None] * 10
+    assert lib.dfmi_gated_delta_tape(*gdn, 1, 4, 2, 4, 48, 8, bf, f32, bf, f32, 0, None) == _lib.DFMI_EINVAL
+    assert b"Dk" in lib.dfmi_last_error()
+    assert lib.dfmi_gated_delta_tape(*gdn, 1, 4, 3, 4, 64, 8, bf, f32, bf, f32, 0, None) == _lib.DFMI_EINVAL
+    assert lib.dfmi_gated_delta_tape(*gdn, 1, 4, 2, 4, 64, 8, 7, f32, bf, f32, 0, None) == _lib.DFMI_EINVAL
+    assert lib.dfmi_gated_delta_tape(*gdn, 1, 4, 2, 4, 64, 8, bf, f32, bf, f32, 0, None) == _lib.DFMI_EINVAL
+    assert b"null" in lib.dfmi_last_error()
+    assert lib.dfmi_gated_delta_tape(*gdn, 0, 4, 2, 4, 64, 8, bf, f32, bf, f32, 0, None) == _lib.DFMI_OK
+    assert lib.dfmi_tape_replay(*([None] * 6), 1, 4, 2, 4, 640, 8, bf, f32, f32, 0, None) == _lib.DFMI_EINVAL
+    assert lib.dfmi_tape_replay(*([None] * 6), 1, 4, 2, 4, 128, 8, bf, f32, f32, 0, None) == _lib.DFMI_EINVAL
 
 
 def test_workspace_queries(lib):

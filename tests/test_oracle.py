@@ -236,3 +236,99 @@ def _case(M, K, N, gs, rng, dtype="bf16"):
     w_q, s, b = oracle.quantize((rng.standard_normal((N, K)) * 0.02).astype(np.float32), gs, 4,
                                 out_dtype=dtype)
     return x, w_q, s, b
+
+
+# --- GDN rollback pair (oracle/gdn.py) -------------------------------------
+
+def _gdn_case(rng, B, T, Hk, Hv, Dk, Dv, vector_g=False):
+    q = rng.standard_normal((B, T, Hk, Dk)).astype(np.float32) / np.sqrt(Dk)
+    k = rng.standard_normal((B, T, Hk, Dk)).astype(np.float32) / np.sqrt(Dk)
+    v = rng.standard_normal((B, T, Hv, Dv)).astype(np.float32)
+    gshape = (B, T, Hv, Dk) if vector_g else (B, T, Hv)
+    g = rng.uniform(0.8, 1.0, size=gshape).astype(np.float32)
+    beta = rng.uniform(0.1, 0.9, size=(B, T, Hv)).astype(np.float32)
+    state = rng.standard_normal((B, Hv, Dv, Dk)).astype(np.float32) * 0.1
+    return q, k, v, g, beta, state
+
+
+@pytest.mark.parametrize("vector_g", [False, True])
+def test_gdn_tape_matches_brute_force_loops(vector_g):
+    rng = np.random.default_rng(1 + vector_g)
+    q, k, v, g, beta, state = _gdn_case(rng, 2, 4, 1, 2, 8, 3, vector_g)
+    mask = np.array([[True, True, False, True], [True, False, True, True]])
+    for m in (None, mask):
+        y, s_out, tape = oracle.gated_delta_with_tape(q, k, v, g, beta, state, m,
+                                                      in_dtype="f32", state_dtype="f32")
+        y2, s2, t2 = oracle.gated_delta_with_tape_loops(q, k, v, g, beta, state, m)
+        assert np.allclose(y, y2, rtol=1e-6, atol=1e-7)
+        assert np.allclose(s_out, s2, rtol=1e-6, atol=1e-7)
+        assert np.allclose(tape, t2, rtol=1e-6, atol=1e-7)
+
+
+def test_gdn_closed_forms():
+    rng = np.random.default_rng(7)
+    q, k, v, g, beta, state = _gdn_case(rng, 1, 3, 2, 4, 8, 5)
+    # beta = 0: no innovation, the state only decays
+    y, s_out, tape = oracle.gated_delta_with_tape(q, k, v, g, np.zeros_like(beta), state,
+                                                  in_dtype="f32", state_dtype="f32")
+    assert not tape.any()
+    decay = np.prod(g[0].astype(np.float64), axis=0)            # [Hv]
+    assert np.allclose(s_out[0], state[0] * decay[:, None, None], rtol=1e-6)
+    hk = np.arange(4) // 2
+    S1 = state[0].astype(np.float64) * g[0, 0][:, None, None]
+    assert np.allclose(y[0, 0], np.einsum("hvk,hk->hv", S1, q[0, 0, hk]), rtol=1e-5, atol=1e-7)
+    # one step from a zero state: S = beta v k^T, y = beta v (k . q)
+    z = np.zeros_like(state)
+    y, s_out, tape = oracle.gated_delta_with_tape(q[:, :1], k[:, :1], v[:, :1], g[:, :1],
+                                                  beta[:, :1], z, in_dtype="f32", state_dtype="f32")
+    bv = beta[0, 0][:, None] * v[0, 0]                           # [Hv, Dv]
+    assert np.allclose(tape[0, 0], bv, rtol=1e-6)
+    assert np.allclose(s_out[0], bv[:, :, None] * k[0, 0, hk][:, None, :], rtol=1e-6, atol=1e-8)
+    kq = np.einsum("hk,hk->h", k[0, 0, hk].astype(np.float64), q[0, 0, hk])
+    assert np.allclose(y[0, 0], bv * kq[:, None], rtol=1e-5, atol=1e-8)
+    # every step masked: nothing moves
+    y, s_out, tape = oracle.gated_delta_with_tape(q, k, v, g, beta, state,
+                                                  np.zeros((1, 3), bool), in_dtype="f32",
+                                                  state_dtype="f32")
+    assert np.array_equal(s_out, state) and not y.any() and not tape.any()
+
+
+@pytest.mark.parametrize("vector_g", [False, True])
+def test_gdn_replay_reproduces_the_accepted_state(vector_g):
+    # the rollback invariant (recurrent_rollback_cache.py:142-165): replaying
+    # the first a+1 steps of the tape from the snapshot gives the state the
+    # recurrence reached after those steps
+    rng = np.random.default_rng(11 + vector_g)
+    q, k, v, g, beta, state = _gdn_case(rng, 1, 6, 2, 4, 16, 8, vector_g)
+    _, s_full, tape = oracle.gated_delta_with_tape(q, k, v, g, beta, state,
+                                                   in_dtype="f32", state_dtype="f32")
+    for acc in (1, 3, 6):
+        _, s_acc, _ = oracle.gated_delta_with_tape(q[:, :acc], k[:, :acc], v[:, :acc], g[:, :acc],
+                                                   beta[:, :acc], state, in_dtype="f32",
+                                                   state_dtype="f32")
+        rep = oracle.tape_replay(tape[:, :acc], k[:, :acc], g[:, :acc], state, k_dtype="f32",
+                                 state_dtype="f32")
+        assert np.allclose(rep, s_acc, rtol=2e-6, atol=1e-7)
+    assert np.allclose(rep, s_full, rtol=2e-6, atol=1e-7)
+
+
+def test_gdn_reference_test_inputs():
+    # the arange-based inputs of the reference's kernel tests
+    # (tests/test_gated_delta_tree_kernel.py:22-54): B=1, T=4, Hk=1, Hv=2,
+    # Dk=32, Dv=4, beta 0.25, g 0.91, zero state; replaying the tape over all
+    # steps gives the recurrence's final state, and bf16 state rounding per
+    # replay step stays within one bf16 step of it
+    q = np.arange(4 * 32, dtype=np.float32).reshape(1, 4, 1, 32) / 100.0
+    k = (np.arange(4 * 32, dtype=np.float32) + 3).reshape(1, 4, 1, 32) / 110.0
+    v = (np.arange(4 * 2 * 4, dtype=np.float32) + 5).reshape(1, 4, 2, 4) / 20.0
+    beta = np.full((1, 4, 2), 0.25, np.float32)
+    state = np.zeros((1, 2, 4, 32), np.float32)
+    for g in (np.full((1, 4, 2), 0.91, np.float32), np.full((1, 4, 2, 32), 0.91, np.float32)):
+        y, s_out, tape = oracle.gated_delta_with_tape(q, k, v, g, beta, state, in_dtype="f32",
+                                                      state_dtype="f32")
+        assert np.all(np.isfinite(y)) and np.abs(s_out).max() > 0
+        rep = oracle.tape_replay(tape, k, g, state, k_dtype="f32", state_dtype="f32")
+        assert np.allclose(rep, s_out, rtol=2e-6, atol=1e-7)
+        rep16 = oracle.to_f32(oracle.tape_replay(tape, k, g, state, k_dtype="f32",
+                                                 state_dtype="bf16"), "bf16")
+        assert np.all(np.abs(rep16 - s_out) <= 2 * 2.0 ** -8 * np.abs(s_out) + 1e-6)
