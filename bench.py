@@ -444,9 +444,9 @@ def run_gdn(args, torch):
     gbs = tape_bytes / (us_tape * 1e-6) / 1e9
     roofline = {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": "gdn_kernel<4, false>", "bytes_per_launch": tape_bytes,
+                "kernel": "gdn_kernel<4, false, 0>", "bytes_per_launch": tape_bytes,
                 "us_per_launch": round(us_tape, 3),
-                "replay": {"kernel": "gdn_kernel<4, true>", "steps": acc + 1,
+                "replay": {"kernel": "gdn_kernel<4, true, 0>", "steps": acc + 1,
                            "bytes_per_launch": rep_bytes, "us_per_launch": round(us_rep, 3),
                            "GBps": round(rep_bytes / (us_rep * 1e-6) / 1e9, 2)}}
     config = {"workload": "GDN rollback pair per layer: gated delta + tape over 16 steps, "

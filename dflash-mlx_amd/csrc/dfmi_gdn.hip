@@ -8,9 +8,12 @@
 // row is a 32-lane half-wavefront, lane j holding elements NPT j .. NPT j +
 // NPT - 1 (NPT = Dk / 32) in registers for all T steps, so the state is read
 // and written once.  The step inputs of a chunk of TC steps are staged in LDS
-// by the whole workgroup first (one memory round trip per chunk instead of
-// one per step); the dot products reduce over the 32 lanes with DPP row
-// operations and one v_permlane16_swap.
+// by the whole workgroup first (every load issued before the first
+// conversion: one memory round trip per chunk), with k . q of each step; the
+// loop reads step t + 1's inputs from LDS while step t computes, its two dot
+// products reduce over the 32 lanes with DPP row operations and one
+// v_permlane16_swap, and the per-step tape entries and outputs go to LDS and
+// leave in one store per chunk.
 // The state is fp32 across the steps of the recurrence; the replay rounds it
 // to the state dtype after every unmasked step, as the reference kernel does.
 #include <algorithm>
@@ -22,13 +25,35 @@ namespace dfmi {
 
 constexpr int kGdnRows = 8;      // state rows per workgroup (one per 32 lanes)
 constexpr int kGdnThreads = 256;
-constexpr int kGdnStageFloats = 16 * 128;  // per staged key / query chunk: TC * Dk
-constexpr int kGdnMaxChunk = kGdnThreads / kGdnRows;  // steps per chunk: one value per thread
+constexpr int kGdnPer = 8;       // elements per thread of a staged key / query / gate chunk
+constexpr int kGdnStageFloats = kGdnThreads * kGdnPer;  // per staged chunk: TC * Dk
+constexpr int kGdnMaxChunk = 32;  // steps per chunk: one live-mask bit each
+// Steps staged per chunk: the key / query / gate chunk fits a stage (TC x 8
+// rows <= 256 threads holds for every TC <= 32: one (step, row) value per
+// thread).
+constexpr int gdn_chunk_steps(int dk) { return std::min(kGdnStageFloats / dk, kGdnMaxChunk); }
 
-__device__ inline float ld_any(const void* p, int64_t i, int dtype) {
-  if (dtype == DFMI_F32) return static_cast<const float*>(p)[i];
-  const uint16_t h = static_cast<const uint16_t*>(p)[i];
-  return dtype == DFMI_BF16 ? Num<BF16>::h2f(h) : Num<F16>::h2f(h);
+// How the replay rounds its state after every step (the state dtype); the
+// recurrence keeps fp32 throughout.
+constexpr int kRoundNone = 0, kRoundBF16 = 1, kRoundF16 = 2;
+
+template <int R>
+__device__ inline float round_state(float v) {
+  if constexpr (R == kRoundBF16) return Num<BF16>::h2f(Num<BF16>::f2h(v));
+  else if constexpr (R == kRoundF16) return Num<F16>::h2f(Num<F16>::f2h(v));
+  else return v;
+}
+
+// One element in its storage form (fp32 bits or a 16-bit value): the load
+// alone, so that all of a thread's loads are issued before the first
+// conversion waits for one.
+__device__ inline uint32_t ld_raw(const void* p, int64_t i, int dtype) {
+  return dtype == DFMI_F32 ? static_cast<const uint32_t*>(p)[i]
+                           : (uint32_t) static_cast<const uint16_t*>(p)[i];
+}
+__device__ inline float cvt_raw(uint32_t r, int dtype) {
+  if (dtype == DFMI_F32) return __uint_as_float(r);
+  return dtype == DFMI_BF16 ? Num<BF16>::h2f(r & 0xFFFFu) : Num<F16>::h2f(r);
 }
 
 __device__ inline void st_any(void* p, int64_t i, int dtype, float v) {
@@ -37,62 +62,126 @@ __device__ inline void st_any(void* p, int64_t i, int dtype, float v) {
   else static_cast<uint16_t*>(p)[i] = Num<F16>::f2h(v);
 }
 
-__device__ inline float round_any(float v, int dtype) {
-  if (dtype == DFMI_BF16) return Num<BF16>::h2f(Num<BF16>::f2h(v));
-  if (dtype == DFMI_F16) return Num<F16>::h2f(Num<F16>::f2h(v));
-  return v;
-}
-
-// Sum over the 32 lanes of a half-wavefront, every lane getting the sum:
-// DPP within each 16-lane row (quad swaps, then half-row and row mirrors),
-// then v_permlane16_swap pairs the two rows of each half-wavefront.
+// Sums over the 32 lanes of a half-wavefront (a state row), every lane
+// getting the sum: DPP within each 16-lane row (quad swaps, then half-row and
+// row mirrors), then v_permlane16_swap pairs the two rows of the
+// half-wavefront.  Two independent sums go through the steps together, so
+// their latencies overlap.
 template <int CTRL>
 __device__ inline float dpp_add_t(float v) {
   return v + __int_as_float(
                  __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
 }
-__device__ inline float sum32(float v) {
-  v = dpp_add_t<0xB1>(v);   // quad_perm [1,0,3,2]
-  v = dpp_add_t<0x4E>(v);   // quad_perm [2,3,0,1]
-  v = dpp_add_t<0x141>(v);  // row_half_mirror
-  v = dpp_add_t<0x140>(v);  // row_mirror: every lane holds its row's sum
+__device__ inline float swap16_add(float v) {
   const auto pr = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
                                                    false);
   return __uint_as_float(pr[0]) + __uint_as_float(pr[1]);
 }
+__device__ inline float swap32_add(float v) {
+  const auto pr = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                   false);
+  return __uint_as_float(pr[0]) + __uint_as_float(pr[1]);
+}
+// Sum over aligned groups of G consecutive lanes (G = 2 .. 64), every lane
+// getting its group's sum.
+template <int G>
+__device__ inline float group_sum(float v) {
+  if constexpr (G >= 2) v = dpp_add_t<0xB1>(v);
+  if constexpr (G >= 4) v = dpp_add_t<0x4E>(v);
+  if constexpr (G >= 8) v = dpp_add_t<0x141>(v);
+  if constexpr (G >= 16) v = dpp_add_t<0x140>(v);
+  if constexpr (G >= 32) v = swap16_add(v);
+  if constexpr (G >= 64) v = swap32_add(v);
+  return v;
+}
+__device__ inline void sum32x2(float& a, float& b) {
+  a = dpp_add_t<0xB1>(a);   // quad_perm [1,0,3,2]
+  b = dpp_add_t<0xB1>(b);
+  a = dpp_add_t<0x4E>(a);   // quad_perm [2,3,0,1]
+  b = dpp_add_t<0x4E>(b);
+  a = dpp_add_t<0x141>(a);  // row_half_mirror
+  b = dpp_add_t<0x141>(b);
+  a = dpp_add_t<0x140>(a);  // row_mirror: every lane holds its row's sum
+  b = dpp_add_t<0x140>(b);
+  a = swap16_add(a);
+  b = swap16_add(b);
+}
 
-// Stage n elements of a [T]-strided source into LDS: element e = t * W + c
-// (t = e / W, c = e % W) comes from src[base + t * stride + c].  Up to
-// kGdnStageFloats / kGdnThreads elements per thread, all loads issued before
-// the first store.
-template <int W>
-__device__ inline void stage(const void* src, int dtype, int64_t base, int64_t stride, int n,
-                            float* dst) {
-  constexpr int PER = kGdnStageFloats / kGdnThreads;
-  float r[PER];
+// A thread's kGdnPer consecutive elements of a staged [nt][DK] chunk (step t
+// from src[base + t * stride ...]), in storage form: 16-byte vector loads when
+// vec (16-byte aligned source: every piece starts at a multiple of 8
+// elements), element loads otherwise; zero past step nt.
+struct Raw8 {
+  u32x4 a, b;  // fp32: eight values; 16-bit: a holds eight, b is unused
+};
+
+template <int DK>
+__device__ inline Raw8 chunk_load(const void* src, int dtype, bool vec, int64_t base,
+                                  int64_t stride, int nt) {
+  Raw8 r;
+  r.a = u32x4{0u, 0u, 0u, 0u};
+  r.b = r.a;
+  const int e0 = threadIdx.x * kGdnPer;
+  const int t = e0 / DK, c = e0 % DK;
+  if (t < nt) {
+    const int64_t i0 = base + (int64_t)t * stride + c;
+    if (dtype == DFMI_F32) {
+      const uint32_t* p = static_cast<const uint32_t*>(src) + i0;
+      if (vec) {
+        r.a = *reinterpret_cast<const u32x4*>(p);
+        r.b = *reinterpret_cast<const u32x4*>(p + 4);
+      } else {
+        r.a = u32x4{p[0], p[1], p[2], p[3]};
+        r.b = u32x4{p[4], p[5], p[6], p[7]};
+      }
+    } else {
+      const uint16_t* p = static_cast<const uint16_t*>(src) + i0;
+      if (vec) {
+        r.a = *reinterpret_cast<const u32x4*>(p);
+      } else {
+        r.a = u32x4{p[0] | (uint32_t)p[1] << 16, p[2] | (uint32_t)p[3] << 16,
+                    p[4] | (uint32_t)p[5] << 16, p[6] | (uint32_t)p[7] << 16};
+      }
+    }
+  }
+  return r;
+}
+
+// The eight elements as floats (lo, hi), also written to dst (16-byte aligned).
+__device__ inline void chunk_store(const Raw8& r, int dtype, float* dst, f32x4& lo, f32x4& hi) {
   if (dtype == DFMI_F32) {
-    const float* p = static_cast<const float*>(src);
+    lo = __builtin_bit_cast(f32x4, r.a);
+    hi = __builtin_bit_cast(f32x4, r.b);
+  } else if (dtype == DFMI_BF16) {
+    lo = f32x4{Num<BF16>::lo(r.a.x), Num<BF16>::hi(r.a.x), Num<BF16>::lo(r.a.y),
+               Num<BF16>::hi(r.a.y)};
+    hi = f32x4{Num<BF16>::lo(r.a.z), Num<BF16>::hi(r.a.z), Num<BF16>::lo(r.a.w),
+               Num<BF16>::hi(r.a.w)};
+  } else {
+    lo = f32x4{Num<F16>::lo(r.a.x), Num<F16>::hi(r.a.x), Num<F16>::lo(r.a.y),
+               Num<F16>::hi(r.a.y)};
+    hi = f32x4{Num<F16>::lo(r.a.z), Num<F16>::hi(r.a.z), Num<F16>::lo(r.a.w),
+               Num<F16>::hi(r.a.w)};
+  }
+  *reinterpret_cast<f32x4*>(dst) = lo;
+  *reinterpret_cast<f32x4*>(dst + 4) = hi;
+}
+
+// NPT floats of one LDS row piece (16-byte aligned when NPT % 4 == 0).
+template <int NPT>
+__device__ inline void lds_piece(const float* p, float (&r)[NPT]) {
+  if constexpr (NPT % 4 == 0) {
 #pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const int e = threadIdx.x + j * kGdnThreads;
-      r[j] = e < n ? p[base + (int64_t)(e / W) * stride + e % W] : 0.f;
+    for (int i = 0; i < NPT; i += 4) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(p + i);
+      r[i] = v.x;
+      r[i + 1] = v.y;
+      r[i + 2] = v.z;
+      r[i + 3] = v.w;
     }
   } else {
-    const uint16_t* p = static_cast<const uint16_t*>(src);
-    uint16_t h[PER];
 #pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const int e = threadIdx.x + j * kGdnThreads;
-      h[j] = e < n ? p[base + (int64_t)(e / W) * stride + e % W] : (uint16_t)0;
-    }
-#pragma unroll
-    for (int j = 0; j < PER; ++j)
-      r[j] = dtype == DFMI_BF16 ? Num<BF16>::h2f(h[j]) : Num<F16>::h2f(h[j]);
-  }
-#pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    const int e = threadIdx.x + j * kGdnThreads;
-    if (e < n) dst[e] = r[j];
+    for (int i = 0; i < NPT; ++i) r[i] = p[i];
   }
 }
 
@@ -125,8 +214,11 @@ __device__ inline void load_row(const void* p, int dtype, int64_t i0, bool vec, 
       return;
     }
   }
+  uint32_t r[NPT];
 #pragma unroll
-  for (int i = 0; i < NPT; ++i) st[i] = ld_any(p, i0 + i, dtype);
+  for (int i = 0; i < NPT; ++i) r[i] = ld_raw(p, i0 + i, dtype);
+#pragma unroll
+  for (int i = 0; i < NPT; ++i) st[i] = cvt_raw(r[i], dtype);
 }
 
 template <int NPT>
@@ -173,25 +265,44 @@ struct GdnArgs {
   int g_per_key;
   int tc;         // steps staged per chunk
   int state_vec;  // state_in / state_out 16-byte (fp32) or 8-byte (16-bit) aligned
+  int kq_vec;     // k (and q) 16-byte aligned
+  int g_vec;      // per-key g 16-byte aligned
 };
 
-// REPLAY = false: gated_delta_tape; true: tape_replay.
-template <int NPT, bool REPLAY>
+// Step inputs of one step, read from LDS one step ahead of their use.
+template <int NPT>
+struct GdnStep {
+  float k[NPT], q[NPT], g[NPT];
+  float v, beta;  // value (replay: tape entry), beta
+  float kq;       // k . q of the step
+};
+
+// REPLAY = false: gated_delta_tape; true: tape_replay (state rounded by RND
+// after every step).  NPT = Dk / 32 state elements per lane.
+template <int NPT, bool REPLAY, int RND>
 __global__ __launch_bounds__(kGdnThreads) void gdn_kernel(GdnArgs a) {
   constexpr int DK = 32 * NPT;
-  __shared__ float s_k[kGdnStageFloats];
-  __shared__ float s_q[REPLAY ? 1 : kGdnStageFloats];
-  __shared__ float s_g[kGdnStageFloats];          // per-key gates (or TC scalars)
-  __shared__ float s_v[kGdnMaxChunk * kGdnRows];  // [TC][8] values or tape entries
+  constexpr int RPW = kGdnRows;
+  __shared__ __attribute__((aligned(16))) float s_k[kGdnStageFloats];
+  __shared__ __attribute__((aligned(16))) float s_q[REPLAY ? 4 : kGdnStageFloats];
+  __shared__ __attribute__((aligned(16))) float s_g[kGdnStageFloats];  // gates, per key
+  __shared__ float s_v[kGdnThreads];  // [TC][RPW] values or tape entries
   __shared__ float s_beta[kGdnMaxChunk];
-  __shared__ int s_live[kGdnMaxChunk];
+  __shared__ float s_kq[kGdnMaxChunk];  // k . q of every step (one key head per workgroup)
+  __shared__ float s_y[REPLAY ? 1 : kGdnThreads];  // [TC][RPW] outputs
+  __shared__ float s_d[REPLAY ? 1 : kGdnThreads];  // [TC][RPW] innovations
+  __shared__ uint32_t s_live;                                  // bit t: step t unmasked
 
   const int bh = blockIdx.y;  // b * Hv + hv
   const int b = bh / a.Hv, hv = bh % a.Hv;
   const int hk = hv / (a.Hv / a.Hk);
-  const int row = threadIdx.x >> 5, lane = threadIdx.x & 31;
-  const int dv = blockIdx.x * kGdnRows + row;
+  const int tid = threadIdx.x;
+  const int row = tid >> 5, lane = tid & 31;
+  const int dv = blockIdx.x * RPW + row;
   const bool have_row = dv < a.Dv;
+  // this thread's (step, row) for the per-step values and outputs
+  const int vt = tid / RPW, vr = tid % RPW;
+  const int vd = blockIdx.x * RPW + vr;
 
   float st[NPT];
   const int64_t srow = ((int64_t)bh * a.Dv + dv) * DK + NPT * lane;
@@ -202,82 +313,164 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_kernel(GdnArgs a) {
   for (int t0 = 0; t0 < a.T; t0 += a.tc) {
     const int nt = min(a.tc, a.T - t0);
     __syncthreads();  // the previous chunk's LDS is no longer read
+    // every load of the chunk's step inputs, then the conversions into LDS
     const int64_t kbase = (((int64_t)b * a.T + t0) * a.Hk + hk) * DK;
-    stage<DK>(a.k, a.x_dtype, kbase, (int64_t)a.Hk * DK, nt * DK, s_k);
-    if (!REPLAY) stage<DK>(a.q, a.x_dtype, kbase, (int64_t)a.Hk * DK, nt * DK, s_q);
+    const int64_t kstride = (int64_t)a.Hk * DK;
     const int64_t hbase = ((int64_t)b * a.T + t0) * a.Hv + hv;  // [b, t0, hv] of [B, T, Hv]
-    if (a.g_per_key) stage<DK>(a.g, a.g_dtype, hbase * DK, (int64_t)a.Hv * DK, nt * DK, s_g);
-    // one value (or tape entry) per thread: rows of this workgroup x steps
-    {
-      const int e = threadIdx.x;  // nt * kGdnRows <= kGdnThreads
-      const int t = e / kGdnRows, r = e % kGdnRows;
-      const int d = blockIdx.x * kGdnRows + r;
-      if (t < nt) {
-        const int64_t vi = (hbase + (int64_t)t * a.Hv) * a.Dv + d;
-        float val = 0.f;
-        if (d < a.Dv) val = REPLAY ? a.tape_in[vi] : ld_any(a.v, vi, a.x_dtype);
-        s_v[e] = val;
-      }
-      if (e < nt) {
-        const int64_t hi = hbase + (int64_t)e * a.Hv;
-        if (!a.g_per_key) s_g[e] = ld_any(a.g, hi, a.g_dtype);
-        if (!REPLAY) s_beta[e] = ld_any(a.beta, hi, a.beta_dtype);
-        s_live[e] = a.mask ? (a.mask[(int64_t)b * a.T + t0 + e] != 0) : 1;
-      }
+    const Raw8 rk = chunk_load<DK>(a.k, a.x_dtype, a.kq_vec != 0, kbase, kstride, nt);
+    Raw8 rq = rk;
+    if constexpr (!REPLAY) rq = chunk_load<DK>(a.q, a.x_dtype, a.kq_vec != 0, kbase, kstride, nt);
+    Raw8 rg = rk;
+    uint32_t rgs = 0;
+    const int tg = tid * kGdnPer / DK;  // step of this thread's gate piece
+    if (a.g_per_key)
+      rg = chunk_load<DK>(a.g, a.g_dtype, a.g_vec != 0, hbase * DK, (int64_t)a.Hv * DK, nt);
+    else if (tg < nt)
+      rgs = ld_raw(a.g, hbase + (int64_t)tg * a.Hv, a.g_dtype);
+    uint32_t rv = 0, rb = 0;
+    bool live = false;
+    if (vt < nt && vd < a.Dv) {
+      const int64_t vi = (hbase + (int64_t)vt * a.Hv) * a.Dv + vd;
+      rv = REPLAY ? __float_as_uint(a.tape_in[vi]) : ld_raw(a.v, vi, a.x_dtype);
+    }
+    if (tid < nt) {
+      if (!REPLAY) rb = ld_raw(a.beta, hbase + (int64_t)tid * a.Hv, a.beta_dtype);
+      live = a.mask ? a.mask[(int64_t)b * a.T + t0 + tid] != 0 : true;
+    }
+    f32x4 klo, khi;
+    chunk_store(rk, a.x_dtype, s_k + tid * kGdnPer, klo, khi);
+    if constexpr (!REPLAY) {
+      // k . q of step tg from the pieces this thread holds: the DK / 8
+      // threads of a step are consecutive lanes of one wavefront
+      f32x4 qlo, qhi;
+      chunk_store(rq, a.x_dtype, s_q + tid * kGdnPer, qlo, qhi);
+      float p = klo.x * qlo.x;
+      p += klo.y * qlo.y;
+      p += klo.z * qlo.z;
+      p += klo.w * qlo.w;
+      p += khi.x * qhi.x;
+      p += khi.y * qhi.y;
+      p += khi.z * qhi.z;
+      p += khi.w * qhi.w;
+      p = group_sum<DK / kGdnPer>(p);
+      if (tid % (DK / kGdnPer) == 0 && tg < nt) s_kq[tg] = p;
+    }
+    if (a.g_per_key) {
+      f32x4 glo, ghi;
+      chunk_store(rg, a.g_dtype, s_g + tid * kGdnPer, glo, ghi);
+    } else {  // the step's scalar gate, repeated over the key dimension
+      const float gv = cvt_raw(rgs, a.g_dtype);
+      *reinterpret_cast<f32x4*>(s_g + tid * kGdnPer) = f32x4{gv, gv, gv, gv};
+      *reinterpret_cast<f32x4*>(s_g + tid * kGdnPer + 4) = f32x4{gv, gv, gv, gv};
+    }
+    if (vt < nt) s_v[tid] = REPLAY ? __uint_as_float(rv) : cvt_raw(rv, a.x_dtype);
+    if (!REPLAY && tid < nt) s_beta[tid] = cvt_raw(rb, a.beta_dtype);
+    if (tid < 64) {  // steps 0 .. nt-1 belong to wavefront 0
+      const uint64_t bal = __ballot(live);
+      if (tid == 0) s_live = (uint32_t)bal;
     }
     __syncthreads();
-    for (int t = 0; t < nt; ++t) {
-      const float* kt = s_k + t * DK + NPT * lane;
-      const float* gt = s_g + (a.g_per_key ? t * DK + NPT * lane : t);
-      const int64_t oi = (((int64_t)b * a.T + t0 + t) * a.Hv + hv) * a.Dv + dv;
-      if (!s_live[t]) {  // uniform: the state stays, tape and output are zero
-        if (!REPLAY && have_row && lane == 0) {
-          a.tape_out[oi] = 0.f;
-          st_any(a.y, oi, a.x_dtype, 0.f);
-        }
-        continue;
+    const uint32_t live_bits = __builtin_amdgcn_readfirstlane(s_live);
+
+    auto fetch = [&](GdnStep<NPT>& in, int t) {
+      lds_piece<NPT>(s_k + t * DK + NPT * lane, in.k);
+      lds_piece<NPT>(s_g + t * DK + NPT * lane, in.g);
+      if constexpr (!REPLAY) {
+        lds_piece<NPT>(s_q + t * DK + NPT * lane, in.q);
+        in.beta = s_beta[t];
+        in.kq = s_kq[t];
       }
+      in.v = s_v[t * RPW + row];
+    };
+    auto advance = [&](const GdnStep<NPT>& in, int t) {
+      const bool on = (live_bits >> t) & 1u;  // uniform
+      if constexpr (REPLAY) {
+        if (on) {
 #pragma unroll
-      for (int i = 0; i < NPT; ++i) st[i] *= a.g_per_key ? gt[i] : gt[0];
-      if (REPLAY) {
-        const float d = s_v[t * kGdnRows + row];
-#pragma unroll
-        for (int i = 0; i < NPT; ++i) st[i] = round_any(st[i] + kt[i] * d, a.state_dtype);
+          for (int i = 0; i < NPT; ++i) {
+            st[i] *= in.g[i];
+            st[i] = round_state<RND>(st[i] + in.k[i] * in.v);
+          }
+        }
       } else {
-        float kv = 0.f;
+        float d = 0.f, o = 0.f;  // a masked step leaves the state; tape and output are zero
+        if (on) {
+          // kv = S'.k and S'.q over the decayed state S'; then
+          // y = (S' + d k^T).q = S'.q + d (k.q), so both sums share one
+          // reduction and k.q comes from the staging
+          float kv = 0.f, sq = 0.f;
 #pragma unroll
-        for (int i = 0; i < NPT; ++i) kv += st[i] * kt[i];
-        kv = sum32(kv);
-        const float d = (s_v[t * kGdnRows + row] - kv) * s_beta[t];
-        const float* qt = s_q + t * DK + NPT * lane;
-        float o = 0.f;
+          for (int i = 0; i < NPT; ++i) {
+            st[i] *= in.g[i];
+            kv += st[i] * in.k[i];
+            sq += st[i] * in.q[i];
+          }
+          sum32x2(kv, sq);
+          d = (in.v - kv) * in.beta;
 #pragma unroll
-        for (int i = 0; i < NPT; ++i) {
-          st[i] += kt[i] * d;
-          o += st[i] * qt[i];
+          for (int i = 0; i < NPT; ++i) st[i] += in.k[i] * d;
+          o = sq + d * in.kq;
         }
-        o = sum32(o);
-        if (have_row && lane == 0) {
-          a.tape_out[oi] = d;
-          st_any(a.y, oi, a.x_dtype, o);
+        if (lane == 0) {
+          s_d[t * RPW + row] = d;
+          s_y[t * RPW + row] = o;
         }
+      }
+    };
+    // two register sets: the LDS reads of step t + 1 are issued before step
+    // t is computed
+    GdnStep<NPT> A, B;
+    fetch(A, 0);
+    // step 0's reads complete before the loop: otherwise the wait the
+    // compiler places for them at the loop head also waits, on every step,
+    // for the reads of the following step
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt, expcnt untouched
+    for (int t = 0; t < nt; t += 2) {
+      if (t + 1 < nt) fetch(B, t + 1);
+      advance(A, t);
+      if (t + 1 >= nt) break;
+      if (t + 2 < nt) fetch(A, t + 2);
+      advance(B, t + 1);
+    }
+    if constexpr (!REPLAY) {
+      __syncthreads();
+      // the chunk's tape entries and outputs: thread -> (step vt, row vr)
+      if (vt < nt && vd < a.Dv) {
+        const int64_t oi = (hbase + (int64_t)vt * a.Hv) * a.Dv + vd;
+        a.tape_out[oi] = s_d[tid];
+        st_any(a.y, oi, a.x_dtype, s_y[tid]);
       }
     }
   }
   if (have_row) store_row<NPT>(a.state_out, a.state_dtype, srow, a.state_vec != 0, st);
 }
 
+template <int NPT>
+static void launch_gdn_npt(const GdnArgs& a, bool replay, hipStream_t st) {
+  const dim3 grid((unsigned)((a.Dv + kGdnRows - 1) / kGdnRows), (unsigned)(a.B * a.Hv));
+  const dim3 blk(kGdnThreads);
+  if (!replay)
+    hipLaunchKernelGGL((gdn_kernel<NPT, false, kRoundNone>), grid, blk, 0, st, a);
+  else if (a.state_dtype == DFMI_BF16)
+    hipLaunchKernelGGL((gdn_kernel<NPT, true, kRoundBF16>), grid, blk, 0, st, a);
+  else if (a.state_dtype == DFMI_F16)
+    hipLaunchKernelGGL((gdn_kernel<NPT, true, kRoundF16>), grid, blk, 0, st, a);
+  else
+    hipLaunchKernelGGL((gdn_kernel<NPT, true, kRoundNone>), grid, blk, 0, st, a);
+}
+
 template <bool REPLAY>
 static void launch_gdn(const GdnArgs& a, hipStream_t st) {
-  const dim3 grid((unsigned)((a.Dv + kGdnRows - 1) / kGdnRows), (unsigned)(a.B * a.Hv));
   switch (a.Dk / 32) {
-    case 1: hipLaunchKernelGGL((gdn_kernel<1, REPLAY>), grid, dim3(kGdnThreads), 0, st, a); break;
-    case 2: hipLaunchKernelGGL((gdn_kernel<2, REPLAY>), grid, dim3(kGdnThreads), 0, st, a); break;
-    case 4: hipLaunchKernelGGL((gdn_kernel<4, REPLAY>), grid, dim3(kGdnThreads), 0, st, a); break;
-    case 8: hipLaunchKernelGGL((gdn_kernel<8, REPLAY>), grid, dim3(kGdnThreads), 0, st, a); break;
-    default: hipLaunchKernelGGL((gdn_kernel<16, REPLAY>), grid, dim3(kGdnThreads), 0, st, a); break;
+    case 1: launch_gdn_npt<1>(a, REPLAY, st); break;
+    case 2: launch_gdn_npt<2>(a, REPLAY, st); break;
+    case 4: launch_gdn_npt<4>(a, REPLAY, st); break;
+    case 8: launch_gdn_npt<8>(a, REPLAY, st); break;
+    default: launch_gdn_npt<16>(a, REPLAY, st); break;
   }
 }
+
+static bool aligned16p(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
 static int gdn_state_vec(const void* in, const void* out, int dtype) {
   const uintptr_t al = dtype == DFMI_F32 ? 16 : 8;
@@ -348,8 +541,10 @@ extern "C" int dfmi_gated_delta_tape(const void* q, const void* k, const void* v
   a.beta_dtype = beta_dtype;
   a.state_dtype = state_dtype;
   a.g_per_key = g_per_key ? 1 : 0;
-  a.tc = std::min(kGdnStageFloats / (int)Dk, kGdnMaxChunk);
+  a.tc = gdn_chunk_steps((int)Dk);
   a.state_vec = gdn_state_vec(state_in, state_out, state_dtype);
+  a.kq_vec = aligned16p(k) && aligned16p(q);
+  a.g_vec = g_per_key && aligned16p(g);
   launch_gdn<false>(a, static_cast<hipStream_t>(stream));
   return check_launch("dfmi_gated_delta_tape");
 }
@@ -385,8 +580,10 @@ extern "C" int dfmi_tape_replay(const float* tape, const void* k, const void* g,
   a.beta_dtype = DFMI_F32;
   a.state_dtype = state_dtype;
   a.g_per_key = g_per_key ? 1 : 0;
-  a.tc = std::min(kGdnStageFloats / (int)Dk, kGdnMaxChunk);
+  a.tc = gdn_chunk_steps((int)Dk);
   a.state_vec = gdn_state_vec(state_in, state_out, state_dtype);
+  a.kq_vec = aligned16p(k);
+  a.g_vec = g_per_key && aligned16p(g);
   launch_gdn<true>(a, static_cast<hipStream_t>(stream));
   return check_launch("dfmi_tape_replay");
 }
