@@ -124,7 +124,7 @@ def cpu_baseline(torch, layer, M):
             ocpu.qmm_bf16(*args, 64, 4, threads)
         reps += 1
         el = time.perf_counter() - t0
-        if el > 8.0 or reps >= 20:
+        if el >= 10.0 or reps >= 400:  # a bounded sample of about 10 s of CPU work
             break
     gbs = total * reps / el / 1e9
     cpu_model = ""
