@@ -59,9 +59,9 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def make_weights(torch, quantize, K, N, gen, dev, gs=64):
+def make_weights(torch, quantize, K, N, gen, dev, gs=64, bits=4):
     w = torch.randn((N, K), generator=gen, device=dev, dtype=torch.float32) * 0.02
-    w_q, s, b = quantize(w, gs, 4, torch.bfloat16)
+    w_q, s, b = quantize(w, gs, bits, torch.bfloat16)
     del w
     return w_q, s, b
 
@@ -182,14 +182,14 @@ def run_sweep(args, torch):
     big = args.workload == "27b"
     shapes = SHAPES_27B if big else SHAPES_9B
     layers = 64 if big else 32
-    M = args.m
+    M, bits = args.m, args.bits
     gen = torch.Generator(device=dev)
     calls = []
     t0 = time.time()
     for l in range(layers):
         gen.manual_seed(100 + l)
         for j, (_, K, N) in enumerate(shapes):
-            w_q, s, b = make_weights(torch, quantize, K, N, gen, dev)
+            w_q, s, b = make_weights(torch, quantize, K, N, gen, dev, bits=bits)
             xg = torch.Generator(device=dev)
             xg.manual_seed(10000 + l * len(shapes) + j)
             x = torch.randn((M, K), generator=xg, device=dev).to(torch.bfloat16)
@@ -197,20 +197,21 @@ def run_sweep(args, torch):
             calls.append((x, w_q, s, b, y))
     torch.cuda.synchronize()
     log(f"weights ready: {len(calls)} matmuls, {time.time() - t0:.1f} s")
-    step_bytes = sum(alg_bytes(M, x.shape[1], w.shape[0]) for (x, w, _, _, _) in calls)
+    step_bytes = sum(alg_bytes(M, x.shape[1], w.shape[0], bits=bits)
+                     for (x, w, _, _, _) in calls)
 
     tuning = None
     if args.path or args.tiles or args.splits:
         tuning = _lib.QmmTuning(args.path, args.tiles, args.splits, args.splits)
     lib = _lib.load()
     tptr = ctypes.byref(tuning) if tuning is not None else None
-    need = max(lib.dfmi_qmm_workspace_bytes_ex(M, x.shape[1], w.shape[0], 64, 4, tptr)
+    need = max(lib.dfmi_qmm_workspace_bytes_ex(M, x.shape[1], w.shape[0], 64, bits, tptr)
                for (x, w, _, _, _) in calls)
 
     def launches(subset):
         def fn():
             for (x, w_q, s, b, y) in subset:
-                qmm_launch(x, w_q, s, b, w_q.shape[0], 64, 4, tuning, out=y)
+                qmm_launch(x, w_q, s, b, w_q.shape[0], 64, bits, tuning, out=y)
         return fn
 
     if args.no_graph:
@@ -238,7 +239,7 @@ def run_sweep(args, torch):
     # dominant kernel: the calls of each kernel replayed alone
     groups = {}
     for c in calls:
-        name = lib.dfmi_qmm_kernel_name(M, c[0].shape[1], c[1].shape[0], 64, 4, tptr).decode()
+        name = lib.dfmi_qmm_kernel_name(M, c[0].shape[1], c[1].shape[0], 64, bits, tptr).decode()
         groups.setdefault(name, []).append(c)
     per_kernel = {}
     reps = max(3, args.steps // 4)
@@ -246,7 +247,8 @@ def run_sweep(args, torch):
         gk = graph_of(torch, launches(subset))
         kms = time_replays(torch, gk, reps)
         del gk
-        kbytes = sum(alg_bytes(M, x.shape[1], w.shape[0]) for (x, w, _, _, _) in subset)
+        kbytes = sum(alg_bytes(M, x.shape[1], w.shape[0], bits=bits)
+                     for (x, w, _, _, _) in subset)
         per_kernel[name] = {"launches_per_step": len(subset), "ms_per_step": round(kms, 4),
                             "us_per_launch": round(kms * 1e3 / len(subset), 3),
                             "bytes_per_launch": kbytes // len(subset),
@@ -260,10 +262,10 @@ def run_sweep(args, torch):
                 "us_per_launch": d["us_per_launch"], "per_kernel": per_kernel}
     config = {"workload": f"{args.workload}-class dense verify-linear sweep",
               "layers": layers, "linears_per_layer": len(shapes), "M": M, "group_size": 64,
-              "bits": 4, "launch": "eager" if args.no_graph else "hip-graph",
+              "bits": bits, "launch": "eager" if args.no_graph else "hip-graph",
               "algorithmic_bytes_per_step": step_bytes}
     res = base_result(args, gbs, ms, len(calls), config, roofline)
-    if not args.no_cpu and args.workload == "9b":
+    if not args.no_cpu and args.workload == "9b" and bits == 4:
         res["cpu_baseline"] = cpu_baseline(torch, calls[:len(shapes)], M)
     return res
 
@@ -486,6 +488,8 @@ def main():
     ap.add_argument("--workload", default="9b",
                     choices=["9b", "27b", "single", "lmhead", "moe", "gdn", "copy"])
     ap.add_argument("--m", type=int, default=16)
+    ap.add_argument("--bits", type=int, default=4, choices=[4, 8],
+                    help="weight bits of the 9b / 27b sweeps")
     ap.add_argument("--path", type=int, default=0, help="1 general kernel, 2 streaming kernel")
     ap.add_argument("--tiles", type=int, default=0)
     ap.add_argument("--splits", type=int, default=0)

@@ -19,6 +19,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace dfmi {
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
@@ -107,6 +109,39 @@ __device__ inline u32x4 dequant_word4(uint32_t w, const DqConst& dq) {
   r.y = __builtin_amdgcn_perm(od, mi, 0x03050100u);  // (q2, q3)
   r.z = __builtin_amdgcn_perm(od, lo, 0x03060302u);  // (q4, q5)
   r.w = __builtin_amdgcn_perm(od, mi, 0x03070302u);  // (q6, q7)
+  return r;
+}
+
+// Two words of 8-bit values (q0..q3, q4..q7, k order, lowest byte first)
+// -> MFMA operand of 8 16-bit values in k order, exactly:
+//   bf16: q -> fp32 (v_cvt_f32_ubyte), whose high half is the bf16 value
+//         (q < 256 has at most 8 significant bits); no offset;
+//   f16:  one byte permute per pair against the magic 0x6400 high bytes:
+//         1024 + q (f16 has 10 mantissa bits); offset 1024.
+template <typename Tag>
+__device__ inline u32x4 dequant_word8(uint32_t w0, uint32_t w1, const DqConst& dq) {
+  u32x4 r;
+  if constexpr (std::is_same<Tag, BF16>::value) {
+    const uint32_t w[2] = {w0, w1};
+    uint32_t d[4];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float f0 = (float)(w[h] & 0xFFu);
+      const float f1 = (float)((w[h] >> 8) & 0xFFu);
+      const float f2 = (float)((w[h] >> 16) & 0xFFu);
+      const float f3 = (float)(w[h] >> 24);
+      // high halves: (f1, f0) and (f3, f2)
+      d[2 * h] = __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
+      d[2 * h + 1] = __builtin_amdgcn_perm(__float_as_uint(f3), __float_as_uint(f2), 0x07060302u);
+    }
+    r = u32x4{d[0], d[1], d[2], d[3]};
+  } else {
+    // selector bytes 0..3 pick bytes of the word, 5 and 7 the magic's 0x64
+    r.x = __builtin_amdgcn_perm(dq.magic, w0, 0x07010500u);  // (q0, q1)
+    r.y = __builtin_amdgcn_perm(dq.magic, w0, 0x07030502u);  // (q2, q3)
+    r.z = __builtin_amdgcn_perm(dq.magic, w1, 0x07010500u);  // (q4, q5)
+    r.w = __builtin_amdgcn_perm(dq.magic, w1, 0x07030502u);  // (q6, q7)
+  }
   return r;
 }
 

@@ -27,12 +27,12 @@ inline int check_launch(const char* what) {
 
 inline size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
-// Shapes the streaming main loop takes (int4): M <= 32, whole 256-k steps and
+// Shapes the streaming main loop takes (int4 or 8-bit): M <= 32, whole 256-k steps and
 // scale blocks of 8 groups; buffer offsets are 32-bit and the record count a
 // signed int, so the packed weights stay under 2 GiB.
-inline bool stream_eligible(int64_t M, int64_t K, int64_t N, int gs) {
+inline bool stream_eligible(int64_t M, int64_t K, int64_t N, int gs, int bits = 4) {
   return M <= 32 && K % 256 == 0 && K % (8 * gs) == 0 && K < (1ll << 24) &&
-         N * (K / 2) < (1ll << 31);
+         N * (K / 8 * bits) < (1ll << 31);
 }
 
 }  // namespace dfmi

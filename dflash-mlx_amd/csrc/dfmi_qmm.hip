@@ -158,9 +158,9 @@ struct StreamArgs {
   int xcd_map;
 };
 
-template <typename Tag, int GS, int MT, int WV>
+template <typename Tag, int GS, int MT, int WV, int BITS, int SBPC>
 __global__ __launch_bounds__(64 * WV) void qmm_stream_kernel(StreamArgs a) {
-  using S = Stream<Tag, GS, MT, WV>;
+  using S = Stream<Tag, GS, MT, WV, SBPC, BITS>;
   constexpr int kThreads = 64 * WV;
   int nb, kpi;
   {
@@ -181,7 +181,7 @@ __global__ __launch_bounds__(64 * WV) void qmm_stream_kernel(StreamArgs a) {
   if (nb >= a.n_blocks) return;  // uniform, before any barrier
   typename S::Ctx cx;
   cx.x = buffer_rsrc(a.x, (uint32_t)a.M * (uint32_t)a.K * 2u);
-  cx.w = buffer_rsrc(a.w, (uint32_t)a.N * (uint32_t)(a.K / 2));
+  cx.w = buffer_rsrc(a.w, (uint32_t)a.N * (uint32_t)(a.K / 8 * BITS));
   cx.s = buffer_rsrc(a.s, (uint32_t)a.N * (uint32_t)(a.K / GS) * 2u);
   cx.b = buffer_rsrc(a.b, (uint32_t)a.N * (uint32_t)(a.K / GS) * 2u);
   cx.K = a.K;
@@ -289,8 +289,15 @@ __global__ __launch_bounds__(64 * WV) void qmm_stream_kernel(StreamArgs a) {
 
 struct StreamPlan {
   int MT, WV, kp, chunks, n_blocks, grid_x, xcd_map, lds;
+  int bits;  // 4 or 8
+  int sbpc;  // scale / bias window pieces (8-bit with 8 wavefronts: 8, to fit LDS)
   size_t ws_bytes;
 };
+
+// Scale / bias window pieces of the streaming kernel: 16, except for 8-bit
+// weights with 8 wavefronts, whose twice-as-long weight stages leave LDS for
+// an 8-piece window only (16 + 48 + 96 KB = 160 KB).
+static int stream_sb_pieces(int bits, int wv) { return bits == 8 && wv == 8 ? 8 : kSbPieces; }
 
 // 8 wavefronts (512-k steps, two wavefronts per SIMD, one workgroup per CU)
 // when K allows and the grid fits on the 256 CUs at once; else 4 wavefronts
@@ -299,8 +306,9 @@ static int stream_waves(int64_t M, int64_t K, int grid) {
   return (M <= 16 && K % 512 == 0 && grid <= 256) ? 8 : 4;
 }
 
-static int plan_stream(int64_t M, int64_t K, int64_t N, int gs, const dfmi_qmm_tuning* tune,
-                       StreamPlan& p) {
+static int plan_stream(int64_t M, int64_t K, int64_t N, int gs, int bits,
+                       const dfmi_qmm_tuning* tune, StreamPlan& p) {
+  p.bits = bits;
   p.MT = M <= 16 ? 1 : 2;
   p.n_blocks = (int)((N + kStreamRows - 1) / kStreamRows);
   int kp;
@@ -321,7 +329,8 @@ static int plan_stream(int64_t M, int64_t K, int64_t N, int gs, const dfmi_qmm_t
   p.chunks = (int)(K / (64 * p.WV));
   p.kp = std::min(p.kp, p.chunks);
   // a split's K range fits one scale / bias window
-  const int max_chunks = sb_max_groups(kSbPieces) / (64 * p.WV / gs);
+  p.sbpc = stream_sb_pieces(bits, p.WV);
+  const int max_chunks = sb_max_groups(p.sbpc) / (64 * p.WV / gs);
   p.kp = std::max(p.kp, (p.chunks + max_chunks - 1) / max_chunks);
   p.xcd_map = (p.n_blocks % 8 == 0) ? 1 : 0;
   p.grid_x = p.n_blocks * p.kp;
@@ -329,21 +338,28 @@ static int plan_stream(int64_t M, int64_t K, int64_t N, int gs, const dfmi_qmm_t
   return DFMI_OK;
 }
 
-template <typename Tag, int GS, int MT, int WV>
+template <typename Tag, int GS, int MT, int WV, int BITS>
 static void launch_stream_t(const StreamPlan& p, hipStream_t st, const StreamArgs& a) {
-  const int lds = Stream<Tag, GS, MT, WV>::LDS_BYTES;
-  hipLaunchKernelGGL((qmm_stream_kernel<Tag, GS, MT, WV>), dim3(p.grid_x), dim3(64 * WV), lds,
-                     st, a);
+  constexpr int SBPC = BITS == 8 && WV == 8 ? 8 : kSbPieces;  // = stream_sb_pieces(BITS, WV)
+  const int lds = Stream<Tag, GS, MT, WV, SBPC, BITS>::LDS_BYTES;
+  hipLaunchKernelGGL((qmm_stream_kernel<Tag, GS, MT, WV, BITS, SBPC>), dim3(p.grid_x),
+                     dim3(64 * WV), lds, st, a);
+}
+
+template <typename Tag, int GS, int BITS>
+static void launch_stream_bits(const StreamPlan& p, hipStream_t st, const StreamArgs& a) {
+  if (p.MT == 1) {
+    if (p.WV == 8) launch_stream_t<Tag, GS, 1, 8, BITS>(p, st, a);
+    else launch_stream_t<Tag, GS, 1, 4, BITS>(p, st, a);
+  } else {
+    launch_stream_t<Tag, GS, 2, 4, BITS>(p, st, a);
+  }
 }
 
 template <typename Tag, int GS>
 static void launch_stream_gs(const StreamPlan& p, hipStream_t st, const StreamArgs& a) {
-  if (p.MT == 1) {
-    if (p.WV == 8) launch_stream_t<Tag, GS, 1, 8>(p, st, a);
-    else launch_stream_t<Tag, GS, 1, 4>(p, st, a);
-  } else {
-    launch_stream_t<Tag, GS, 2, 4>(p, st, a);
-  }
+  if (p.bits == 8) launch_stream_bits<Tag, GS, 8>(p, st, a);
+  else launch_stream_bits<Tag, GS, 4>(p, st, a);
 }
 
 template <typename Tag>
@@ -354,30 +370,37 @@ static void launch_stream(int gs, const StreamPlan& p, hipStream_t st, const Str
 }
 
 // Dynamic LDS above 64 KiB needs the per-kernel attribute raised once.
-template <typename Tag, int GS, int MT, int WV>
+template <typename Tag, int GS, int MT, int WV, int BITS>
 static void allow_lds_t() {
-  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&qmm_stream_kernel<Tag, GS, MT, WV>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize,
-                            Stream<Tag, GS, MT, WV>::LDS_BYTES);
+  constexpr int SBPC = BITS == 8 && WV == 8 ? 8 : kSbPieces;
+  (void)hipFuncSetAttribute(
+      reinterpret_cast<const void*>(&qmm_stream_kernel<Tag, GS, MT, WV, BITS, SBPC>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, Stream<Tag, GS, MT, WV, SBPC, BITS>::LDS_BYTES);
 }
 
 template <typename Tag, int GS>
 static void allow_lds_gs() {
-  allow_lds_t<Tag, GS, 1, 4>();
-  allow_lds_t<Tag, GS, 1, 8>();
-  allow_lds_t<Tag, GS, 2, 4>();
+  allow_lds_t<Tag, GS, 1, 4, 4>();
+  allow_lds_t<Tag, GS, 1, 8, 4>();
+  allow_lds_t<Tag, GS, 2, 4, 4>();
+  allow_lds_t<Tag, GS, 1, 4, 8>();
+  allow_lds_t<Tag, GS, 1, 8, 8>();
+  allow_lds_t<Tag, GS, 2, 4, 8>();
 }
 
 static void allow_lds_all() {
-  static bool done = false;  // benign race: the attribute calls are idempotent
-  if (done) return;
-  allow_lds_gs<BF16, 32>();
-  allow_lds_gs<BF16, 64>();
-  allow_lds_gs<BF16, 128>();
-  allow_lds_gs<F16, 32>();
-  allow_lds_gs<F16, 64>();
-  allow_lds_gs<F16, 128>();
-  done = true;
+  // once per process (thread-safe static initialisation); the attribute
+  // calls are idempotent
+  static const bool done = [] {
+    allow_lds_gs<BF16, 32>();
+    allow_lds_gs<BF16, 64>();
+    allow_lds_gs<BF16, 128>();
+    allow_lds_gs<F16, 32>();
+    allow_lds_gs<F16, 64>();
+    allow_lds_gs<F16, 128>();
+    return true;
+  }();
+  (void)done;
 }
 
 // ---------------------------------------------------------------------------
@@ -535,28 +558,30 @@ static bool use_direct(int64_t M, int64_t K, int64_t N, int gs, int bits,
 static bool use_stream(int64_t M, int64_t K, int64_t N, int gs, int bits,
                        const dfmi_qmm_tuning* tune) {
   const int path = tune ? tune->path : 0;
-  if (bits != 4) return false;
+  if (bits != 4 && bits != 8) return false;
   if (path == 1 || path == 3) return false;
-  // more blocks than split counters run unsplit: the whole K in one scale window
-  return stream_eligible(M, K, N, gs) &&
-         ((N + kStreamRows - 1) / kStreamRows <= kMaxCounters || K / gs <= sb_max_groups(kSbPieces));
+  // more blocks than split counters run unsplit: the whole K in one scale
+  // window (8-bit: the smaller window of its plans)
+  const int sbpc = bits == 8 ? 8 : kSbPieces;
+  return stream_eligible(M, K, N, gs, bits) &&
+         ((N + kStreamRows - 1) / kStreamRows <= kMaxCounters || K / gs <= sb_max_groups(sbpc));
 }
 
 extern "C" size_t dfmi_qmm_workspace_bytes_ex(int64_t M, int64_t K, int64_t N, int group_size,
                                               int bits, const dfmi_qmm_tuning* tuning) {
-  if (validate_qmm(DFMI_BF16, M, K, N, group_size, bits) != DFMI_OK || M == 0 || N == 0 ||
-      bits != 4)
+  if (validate_qmm(DFMI_BF16, M, K, N, group_size, bits) != DFMI_OK || M == 0 || N == 0)
     return 0;
   if (!use_stream(M, K, N, group_size, bits, tuning)) return 0;
   StreamPlan p;
-  if (plan_stream(M, K, N, group_size, tuning, p) != DFMI_OK) return 0;
+  if (plan_stream(M, K, N, group_size, bits, tuning, p) != DFMI_OK) return 0;
   return p.ws_bytes;
 }
 
 extern "C" const char* dfmi_qmm_kernel_name(int64_t M, int64_t K, int64_t N, int group_size,
                                              int bits, const dfmi_qmm_tuning* tuning) {
   if (validate_qmm(DFMI_BF16, M, K, N, group_size, bits) != DFMI_OK) return nullptr;
-  if (bits == 8) return "qmm8_kernel";
+  if (bits == 8) return use_stream(M, K, N, group_size, bits, tuning) ? "qmm8_stream_kernel"
+                                                                      : "qmm8_kernel";
   if (use_direct(M, K, N, group_size, bits, tuning)) return "qmm_direct_kernel";
   return use_stream(M, K, N, group_size, bits, tuning) ? "qmm_stream_kernel" : "qmm_dense_kernel";
 }
@@ -583,8 +608,9 @@ extern "C" int dfmi_qmm_affine_ex(const void* x, int x_dtype, const uint32_t* w_
     return DFMI_EINVAL;
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (bits == 8) return dfmi_qmm8_launch(x, x_dtype, w_q, scales, biases, y, M, K, N, group_size,
-                                         stream);
+  // 8-bit: the streaming kernel where it applies, else the register-load kernel
+  if (bits == 8 && !use_stream(M, K, N, group_size, bits, tuning))
+    return dfmi_qmm8_launch(x, x_dtype, w_q, scales, biases, y, M, K, N, group_size, stream);
   if (tuning && tuning->path == 2 && !stream_eligible(M, K, N, group_size)) {
     set_error("dfmi_qmm: shape M=%lld K=%lld gs=%d outside the streaming kernel", (long long)M,
               (long long)K, group_size);
@@ -614,7 +640,7 @@ extern "C" int dfmi_qmm_affine_ex(const void* x, int x_dtype, const uint32_t* w_
   }
   if (use_stream(M, K, N, group_size, bits, tuning)) {
     StreamPlan p;
-    rc = plan_stream(M, K, N, group_size, tuning, p);
+    rc = plan_stream(M, K, N, group_size, bits, tuning, p);
     if (rc != DFMI_OK) return rc;
     StreamArgs a;
     a.x = static_cast<const uint16_t*>(x);

@@ -93,7 +93,7 @@ __device__ inline uint32_t opaque(uint32_t v) {
   return v;
 }
 
-template <typename Tag, int GS, int MT, int WV, int SBPC = kSbPieces>
+template <typename Tag, int GS, int MT, int WV, int SBPC = kSbPieces, int BITS = 4>
 struct Stream {
   static constexpr int NT = kStreamTiles;
   static constexpr int NB = kStreamRows;
@@ -101,9 +101,18 @@ struct Stream {
   static constexpr int GPC = CK / GS;       // quantisation groups per step
   static constexpr int XROW = CK * 2;       // bytes of one activation row per step
   static constexpr int XPPR = CK / 8;       // 16-byte pieces per activation row
-  static constexpr int WROW = CK / 2;       // bytes of one weight row per step
+  static constexpr int WPK = BITS / 4;      // 32-bit words per 8-k piece of a weight row
+  static constexpr int WROW = CK * BITS / 8;  // bytes of one weight row per step
   static constexpr int WPPR = WROW / 16;    // 16-byte pieces per weight row
+  // weight-stage swizzle key: row % SWZ (at most 16, so a tile's rows share
+  // the keys of tile 0 whatever the row length)
+  static constexpr int SWZ = WPPR < 16 ? WPPR : 16;
   static_assert(WV == 4 || WV == 8, "wavefronts");
+  static_assert(BITS == 4 || BITS == 8, "weight bits");
+  // 8-bit values are dequantised exactly: bf16 by conversion (no offset),
+  // f16 by the 1024 magic
+  static constexpr float OFFQ =
+      BITS == 4 ? Num<Tag>::OFF : (std::is_same<Tag, BF16>::value ? 0.f : 1024.f);
   // LDS stages (DEPTH - 1 steps in flight).  Four stages with 8 wavefronts
   // measured slower than three on MI355X (4096x12288: 12.8 us vs 11.4 us):
   // the extra step in flight does not raise the per-CU request rate, and the
@@ -177,8 +186,8 @@ struct Stream {
 
   // One step's operands of this lane, read from LDS.
   struct Frag {
-    u32x4 x[MT][2];     // activations of k-block j
-    uint32_t w[NT][2];  // packed words of k-block j
+    u32x4 x[MT][2];           // activations of k-block j
+    uint32_t w[NT][2 * WPK];  // packed words of k-block j: w[t][WPK j .. WPK j + WPK - 1]
     uint32_t sv[NT];    // dword holding this lane's scale(s)
     uint32_t bv[NT];    // dword holding this lane's bias(es)
   };
@@ -207,23 +216,23 @@ struct Stream {
       L.xg[i] = r < cx.M ? (uint32_t)xr * (uint32_t)cx.K * 2u + (uint32_t)piece * 16u : kNoRow;
     }
     // weight stage: instruction i of wavefront w covers 64 / WPPR consecutive
-    // rows; lane l loads piece (l % WPPR) ^ (row % WPPR) of its row into slot
+    // rows; lane l loads piece (l % WPPR) ^ (row % SWZ) of its row into slot
     // l % WPPR; rows >= N re-read row N-1
     constexpr int RPI = 64 / WPPR;
 #pragma unroll
     for (int i = 0; i < W_DMA; ++i) {
       const int r = (cx.wave * W_DMA + i) * RPI + cx.lane / WPPR;
-      const int piece = (cx.lane % WPPR) ^ (r % WPPR);
+      const int piece = (cx.lane % WPPR) ^ (r % SWZ);
       const int n = min(cx.n0 + (r >= cx.split ? r - cx.split : r), cx.N - 1);
-      L.wg[i] = (uint32_t)n * (uint32_t)(cx.K / 2) + (uint32_t)piece * 16u;
+      L.wg[i] = (uint32_t)n * (uint32_t)(cx.K / 8 * BITS) + (uint32_t)piece * 16u;
     }
     // fragment reads (row m = col of M-block 0, row r = col of tile 0; the
     // other blocks / tiles are whole-row multiples away)
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       L.xo[j] = (uint32_t)(col * XROW + ((piece_of(cx.wave, kg, j) ^ col) * 16));
-      const int byte = piece_of(cx.wave, kg, j) * 4;
-      L.wo[j] = (uint32_t)(col * WROW + (((byte >> 4) ^ (col % WPPR)) * 16) + (byte & 15));
+      const int byte = piece_of(cx.wave, kg, j) * 4 * WPK;
+      L.wo[j] = (uint32_t)(col * WROW + (((byte >> 4) ^ (col % SWZ)) * 16) + (byte & 15));
     }
     L.sbr = (uint32_t)(col * SBP);
     L.swz = (uint32_t)(col % SBPC);
@@ -240,7 +249,7 @@ struct Stream {
   }
 
   __device__ static inline void issue_w(const Ctx& cx, const Lane& L, int c, int stage) {
-    const uint32_t u = (uint32_t)c * (uint32_t)(CK / 2);
+    const uint32_t u = (uint32_t)c * (uint32_t)WROW;
     constexpr int RPI = 64 / WPPR;
 #pragma unroll
     for (int i = 0; i < W_DMA; ++i) {
@@ -303,13 +312,26 @@ struct Stream {
         dfmi_smem + SB_OFF + (L.sbr + (((gr >> 3) ^ L.swz) << 4) + ((gr & 7) >> 1) * 4);
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      if constexpr (PAIR) {
+      if constexpr (PAIR && BITS == 4) {
         const u32x2 v = *reinterpret_cast<const u32x2*>(ws0 + t * 16 * WROW);
         f.w[t][0] = v.x;
         f.w[t][1] = v.y;
-      } else {
+      } else if constexpr (PAIR) {  // 8-bit: both k-blocks in one 16-byte piece
+        const u32x4 v = *reinterpret_cast<const u32x4*>(ws0 + t * 16 * WROW);
+        f.w[t][0] = v.x;
+        f.w[t][1] = v.y;
+        f.w[t][2] = v.z;
+        f.w[t][3] = v.w;
+      } else if constexpr (BITS == 4) {
         f.w[t][0] = *reinterpret_cast<const uint32_t*>(ws0 + t * 16 * WROW);
         f.w[t][1] = *reinterpret_cast<const uint32_t*>(ws1 + t * 16 * WROW);
+      } else {
+        const u32x2 v0 = *reinterpret_cast<const u32x2*>(ws0 + t * 16 * WROW);
+        const u32x2 v1 = *reinterpret_cast<const u32x2*>(ws1 + t * 16 * WROW);
+        f.w[t][0] = v0.x;
+        f.w[t][1] = v0.y;
+        f.w[t][2] = v1.x;
+        f.w[t][3] = v1.y;
       }
       f.sv[t] = *reinterpret_cast<const uint32_t*>(sbp + t * 16 * SBP);
       f.bv[t] = *reinterpret_cast<const uint32_t*>(sbp + t * 16 * SBP + NB * SBP);
@@ -345,11 +367,17 @@ struct Stream {
     }
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      const u32x4 b0 = dequant_word4<Tag>(f.w[t][0], dq);
-      const u32x4 b1 = dequant_word4<Tag>(f.w[t][1], dq);
+      u32x4 b0, b1;
+      if constexpr (BITS == 4) {
+        b0 = dequant_word4<Tag>(f.w[t][0], dq);
+        b1 = dequant_word4<Tag>(f.w[t][1], dq);
+      } else {
+        b0 = dequant_word8<Tag>(f.w[t][0], f.w[t][1], dq);
+        b1 = dequant_word8<Tag>(f.w[t][2], f.w[t][3], dq);
+      }
       if constexpr (PAIR) {
         const float s = half_of(f.sv[t], L.hsel);
-        const float bq = __builtin_fmaf(-Num<Tag>::OFF, s, half_of(f.bv[t], L.hsel));
+        const float bq = __builtin_fmaf(-OFFQ, s, half_of(f.bv[t], L.hsel));
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
           const f32x4 p = Num<Tag>::mma(f.x[mt][1], b1, Num<Tag>::mma(f.x[mt][0], b0, zero4()));
@@ -362,7 +390,7 @@ struct Stream {
         for (int j = 0; j < 2; ++j) {
           const uint32_t sel = j ? 0x03020c0cu : 0x01000c0cu;
           const float s = half_of(f.sv[t], sel);
-          const float bq = __builtin_fmaf(-Num<Tag>::OFF, s, half_of(f.bv[t], sel));
+          const float bq = __builtin_fmaf(-OFFQ, s, half_of(f.bv[t], sel));
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) {
             const f32x4 p = Num<Tag>::mma(f.x[mt][j], j ? b1 : b0, zero4());

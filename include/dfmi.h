@@ -103,7 +103,8 @@ int dfmi_qmm_affine_ex(const void *x, int x_dtype, const uint32_t *w_q, const vo
 size_t dfmi_qmm_workspace_bytes(int64_t M, int64_t K, int64_t N, int group_size, int bits);
 /* Host-only plan query (no reference counterpart; for benchmarks and
  * profiles): name of the kernel dfmi_qmm_affine_ex would launch for this
- * shape, "qmm_stream_kernel", "qmm_dense_kernel" or (bits 8) "qmm8_kernel";
+ * shape, "qmm_stream_kernel", "qmm_dense_kernel" or (bits 8)
+ * "qmm8_stream_kernel" / "qmm8_kernel";
  * NULL if unsupported. */
 const char *dfmi_qmm_kernel_name(int64_t M, int64_t K, int64_t N, int group_size, int bits,
                                  const dfmi_qmm_tuning *tuning);

@@ -208,8 +208,14 @@ def test_unsupported_raises(dev):
         vq.quantized_matmul(xf, w[:, :8], s[:, :1], s[:, :1], group_size=64, bits=4)
 
 
-@pytest.mark.parametrize("M,K,N,gs", [(16, 4096, 1024, 64), (4, 512, 96, 32), (16, 1024, 2048, 128),
-                                      (33, 256, 40, 64), (1, 96, 16, 32)])
+@pytest.mark.parametrize("M,K,N,gs", [
+    (16, 4096, 1024, 64),   # streaming, 8 wavefronts, K split 4 ways
+    (4, 512, 96, 32),       # streaming, 8 wavefronts, one step, ragged N
+    (16, 1024, 2048, 128),  # streaming, 8 wavefronts
+    (24, 2048, 200, 64),    # streaming, 4 wavefronts, two 16-row activation blocks
+    (16, 512, 16448, 64),   # streaming, 4 wavefronts (257 blocks), unsplit
+    (33, 256, 40, 64),      # register-load kernel (M > 32)
+    (1, 96, 16, 32)])       # register-load kernel (K not whole 256-k steps)
 @pytest.mark.parametrize("dtype", ["bf16", "f16"])
 def test_8bit_matches_oracle(dev, M, K, N, gs, dtype):
     """bits=8 (the reference's mma2big_8bit layout, verify_qmm.py:593-598)."""
@@ -220,19 +226,24 @@ def test_8bit_matches_oracle(dev, M, K, N, gs, dtype):
     assert rel <= 1e-2, rel
 
 
-def test_8bit_closed_form_exact(dev):
+@pytest.mark.parametrize("K", [256, 1024])  # register-load kernel, streaming kernel
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_8bit_closed_form_exact(dev, K, dtype):
     """Integer activations, unit scales, small integer biases: the fp32 result is
-    exact, so the 8-bit path must be bit-exact after rounding."""
-    import torch
-
+    exact, so the 8-bit path must be bit-exact after rounding (every code
+    0..255 occurs, so the exact bf16 conversion and the f16 magic are both
+    pinned)."""
     rng = np.random.default_rng(8)
-    M, K, N, gs = 16, 256, 64, 64
+    M, N, gs = 16, 64, 64
     q = rng.integers(0, 256, size=(N, K))
+    q[0, :256] = np.arange(256)
     w_q = oracle.pack(q, 8)
-    s = oracle.round_to_dtype(np.ones((N, K // gs), np.float32), "bf16")
-    b = oracle.round_to_dtype(rng.integers(-2, 3, size=(N, K // gs)).astype(np.float32), "bf16")
-    x = oracle.round_to_dtype(rng.integers(-2, 3, size=(M, K)).astype(np.float32), "bf16")
-    want = oracle.quantized_matmul(x, w_q, s, b, group_size=gs, bits=8, dtype="bf16",
-                                   out_dtype="bf16")
-    got = _run(dev, x, w_q, s, b, gs, bits=8)
+    s = oracle.round_to_dtype(np.ones((N, K // gs), np.float32), dtype)
+    b = oracle.round_to_dtype(rng.integers(-2, 3, size=(N, K // gs)).astype(np.float32), dtype)
+    x = oracle.round_to_dtype(rng.integers(-1, 2, size=(M, K)).astype(np.float32), dtype)
+    exact = oracle.quantized_matmul(x, w_q, s, b, group_size=gs, bits=8, dtype=dtype)
+    assert np.abs(exact).max() < 6e4  # inside the f16 range: the test is well posed
+    want = oracle.quantized_matmul(x, w_q, s, b, group_size=gs, bits=8, dtype=dtype,
+                                   out_dtype=dtype)
+    got = _run(dev, x, w_q, s, b, gs, dtype=dtype, bits=8)
     assert np.array_equal(got, want)
