@@ -59,12 +59,16 @@ class _WorkspaceCache:
     The kernels leave every counter they touch at zero, so a buffer is
     zero-filled only when it is created or grown.  Growing is not allowed
     while a HIP graph is being captured: reserve the size beforehand
-    (``reserve``), e.g. through ``prewarm_verify_kernels``.
+    (``reserve``), e.g. through ``prewarm_verify_kernels``.  A buffer that a
+    larger one replaces stays allocated: a graph captured earlier still
+    launches kernels on its address (each replacement at least doubles the
+    size, so the retired buffers total less than the live one).
     """
 
     def __init__(self):
         self._lock = threading.Lock()
         self._bufs: dict[tuple[int, int, str], torch.Tensor] = {}
+        self._retired: list[torch.Tensor] = []
 
     def get(self, device: torch.device, nbytes: int, kind: str = "qmm") -> torch.Tensor:
         nbytes = max(int(nbytes), 256)
@@ -78,6 +82,8 @@ class _WorkspaceCache:
                         f"libdfmi workspace must grow to {nbytes} bytes during graph capture; "
                         "reserve it before capturing")
                 size = max(nbytes, 2 * (buf.numel() if buf is not None else 0))
+                if buf is not None:
+                    self._retired.append(buf)
                 buf = torch.zeros(size + 256, dtype=torch.uint8, device=device)
                 self._bufs[key] = buf
         return buf

@@ -247,3 +247,44 @@ def test_8bit_closed_form_exact(dev, K, dtype):
                                    out_dtype=dtype)
     got = _run(dev, x, w_q, s, b, gs, dtype=dtype, bits=8)
     assert np.array_equal(got, want)
+
+
+def test_captured_graph_survives_workspace_growth(dev):
+    """A graph captured with a split-K call keeps its workspace address: a
+    later, larger call on the same stream grows the stream's workspace, the
+    old buffer must stay allocated (the replay still writes partials and
+    counters there), and memory handed out afterwards stays untouched."""
+    import torch
+
+    from dflash_mlx_amd import verify_qmm as vq
+
+    M, K, N, gs = 16, 4096, 1024, 64  # K split over 4 workgroups: uses the workspace
+    x, w_q, s, b = make_qmm_case(M, K, N, gs, seed=21)
+    xt, wt, st_, bt = to_dev(x, "bf16", dev), to_dev(w_q, "u32", dev), to_dev(s, "bf16", dev), \
+        to_dev(b, "bf16", dev)
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        vq.quantized_matmul(xt, wt, st_, bt, group_size=gs)  # creates this stream's workspace
+    stream.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        yg = vq.quantized_matmul(xt, wt, st_, bt, group_size=gs)
+    # a larger split-K call on the same stream grows the workspace
+    K2, N2 = 12288, 4096  # 4 splits: 1 MiB of partials against 256 KiB
+    with torch.cuda.stream(stream):  # (values irrelevant: only the workspace size matters)
+        vq.quantized_matmul(torch.zeros((M, K2), dtype=torch.bfloat16, device=dev),
+                            torch.zeros((N2, K2 // 8), dtype=torch.int32, device=dev),
+                            torch.zeros((N2, K2 // gs), dtype=torch.bfloat16, device=dev),
+                            torch.zeros((N2, K2 // gs), dtype=torch.bfloat16, device=dev),
+                            group_size=gs)
+    stream.synchronize()
+    fills = [torch.full((1 << 18,), 7, dtype=torch.int32, device=dev) for _ in range(16)]
+    torch.cuda.synchronize()
+    want = oracle.quantized_matmul(x, w_q, s, b, group_size=gs, dtype="bf16")
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        _check(from_dev(yg, "bf16"), x, w_q, s, b, gs)
+        _, rel = oracle.parity_metrics(oracle.to_f32(from_dev(yg, "bf16"), "bf16"), want)
+        assert rel <= REL_TOL
+    assert all(bool((f == 7).all()) for f in fills)
