@@ -371,6 +371,7 @@ def run_moe(args, torch):
 
     lay = []
     total = 0
+    sw_bytes = dn_bytes = 0  # algorithmic bytes of the gate/up and the down launches
     for _ in range(layers):
         gate, up, down = experts(I, D), experts(I, D), experts(D, I)
         logits = torch.randn((T, E), generator=gen, device=dev)
@@ -385,7 +386,10 @@ def run_moe(args, torch):
         inv[order] = torch.arange(order.numel(), device=dev)
         inv = inv.to(torch.int32)  # row of each pair in the expert-sorted outputs
         n_e = int(torch.unique(flat).numel())
-        total += n_e * 3 * (I * D // 2 + 4 * I * D // 64) + 2 * T * D * 2
+        per_expert = I * D // 2 + 4 * I * D // 64
+        total += n_e * 3 * per_expert + 2 * T * D * 2
+        sw_bytes += n_e * 2 * per_expert + T * D * 2 + T * k * I * 2
+        dn_bytes += n_e * per_expert + T * k * I * 2 + T * k * D * 2
         x = torch.randn((T, D), generator=gen, device=dev).to(torch.bfloat16)
         lay.append((gate, up, down, rhs, lhs, inv, sc, x))
     log(f"moe weights ready ({layers} layers)")
@@ -399,10 +403,38 @@ def run_moe(args, torch):
     g = graph_of(torch, fn)
     ms = time_replays(torch, g, args.steps, warmup=args.warmup)
     gbs = total / (ms * 1e-3) / 1e9
-    roofline = {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(gbs / HBM_PEAK_GBS, 4),
-                "traffic": measured_traffic("moe", "gather_kernel"), "kernel": "gather_kernel",
-                "bytes_per_launch": total // (2 * layers), "us_per_launch": None}
+    del g
+
+    # each gather kernel's launches replayed alone (the gate/up SwiGLU pair
+    # dominates: two thirds of the weight bytes)
+    hs = [gather_swiglu(x, gate, up, rhs, lhs_indices=lhs, group_size=64)
+          for (gate, up, down, rhs, lhs, inv, sc, x) in lay]
+
+    def fn_sw():
+        for (gate, up, down, rhs, lhs, inv, sc, x) in lay:
+            gather_swiglu(x, gate, up, rhs, lhs_indices=lhs, group_size=64)
+
+    def fn_dn():
+        for h, (gate, up, down, rhs, lhs, inv, sc, x) in zip(hs, lay):
+            gather_qmm(h, *down, rhs, group_size=64)
+
+    reps = max(3, args.steps // 4)
+    per_kernel = {}
+    for name, f, nbytes in (("gather_persist_kernel", fn_sw, sw_bytes),
+                            ("gather_kernel", fn_dn, dn_bytes)):
+        gk = graph_of(torch, f)
+        kms = time_replays(torch, gk, reps)
+        del gk
+        per_kernel[name] = {"launches_per_step": layers, "ms_per_step": round(kms, 4),
+                            "us_per_launch": round(kms * 1e3 / layers, 3),
+                            "bytes_per_launch": nbytes // layers,
+                            "GBps": round(nbytes / (kms * 1e-3) / 1e9, 2)}
+    dom = per_kernel["gather_persist_kernel"]
+    roofline = {"bound": "hbm", "achieved": dom["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(dom["GBps"] / HBM_PEAK_GBS, 4),
+                "traffic": measured_traffic("moe", "gather_persist_kernel"),
+                "kernel": "gather_persist_kernel", "bytes_per_launch": dom["bytes_per_launch"],
+                "us_per_launch": dom["us_per_launch"], "per_kernel": per_kernel}
     config = {"workload": "MoE 40 layers, 16 tokens top-8 of 256 experts, hidden 2048, "
                           "expert width 512, int4 gs64", "algorithmic_bytes_per_step": total}
     return base_result(args, gbs, ms, 3 * layers, config, roofline)

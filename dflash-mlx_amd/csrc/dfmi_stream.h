@@ -127,8 +127,10 @@ struct Stream {
   // before its first step: [array][row][SBP bytes], a row's window of 16-byte
   // pieces (8 groups each) XOR-swizzled by row.  Up to SBPC pieces, i.e. a
   // K range of at most MAX_GROUPS groups (any start).
-  static_assert(SBPC == 8 || SBPC == 16, "scale window pieces");
+  // (4 pieces only for windows that start at group 0: K / GS <= 32)
+  static_assert(SBPC == 4 || SBPC == 8 || SBPC == 16, "scale window pieces");
   static constexpr int MAX_GROUPS = sb_max_groups(SBPC);
+  static constexpr int SBPC_N = SBPC;         // pieces per row and array
   static constexpr int SBP = 16 * SBPC;        // bytes per row and array
   static constexpr int SBBUF = 2 * NB * SBP;   // scales, then biases
   // Scale / bias region first: its fragment reads use immediate offsets
@@ -161,6 +163,7 @@ struct Stream {
     int groups;  // K / GS
     int n0;      // first weight row of this workgroup (in each weight set)
     int wave, lane;
+    uint32_t sb_base;  // LDS offset of this run's scale / bias window (past SB_OFF)
 
     // Dense defaults: activation rows 0 .. M-1, one weight set.
     __device__ inline void dense() {
@@ -170,6 +173,7 @@ struct Stream {
       w2 = w;
       s2 = s;
       b2 = b;
+      sb_base = 0;
     }
   };
 
@@ -280,7 +284,7 @@ struct Stream {
               ? ((uint32_t)n * (uint32_t)cx.groups + (uint32_t)(piece0 + q) * 8u) * 2u
               : kNoRow;
       const __amdgpu_buffer_rsrc_t src = arr ? (second ? cx.b2 : cx.b) : (second ? cx.s2 : cx.s);
-      dma16(src, off, 0u, dfmi_smem + SB_OFF + arr * NB * SBP + r0 * SBP);
+      dma16(src, off, 0u, dfmi_smem + SB_OFF + cx.sb_base + arr * NB * SBP + r0 * SBP);
     }
   }
 
@@ -308,8 +312,8 @@ struct Stream {
     // (gr / 8) ^ (col % SBPC)), dword (gr % 8) / 2 of the piece
     const uint32_t gr =
         (uint32_t)(c * GPC + (PAIR ? (cx.wave * 64) / GS : 2 * cx.wave) - g0w);
-    const char* sbp =
-        dfmi_smem + SB_OFF + (L.sbr + (((gr >> 3) ^ L.swz) << 4) + ((gr & 7) >> 1) * 4);
+    const char* sbp = dfmi_smem + SB_OFF + cx.sb_base +
+                      (L.sbr + (((gr >> 3) ^ L.swz) << 4) + ((gr & 7) >> 1) * 4);
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       if constexpr (PAIR && BITS == 4) {

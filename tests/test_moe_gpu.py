@@ -69,14 +69,19 @@ def test_gather_qmm_matches_oracle(dev, dtype, gs, sort):
     _check(from_dev(got, dtype), want, dtype)
 
 
-@pytest.mark.parametrize("K,N", [(320, 40), (2048, 512), (512, 2048), (96, 16)])
-def test_gather_qmm_shapes(dev, K, N):
-    """Ragged K (tail chunk) and N (partial tile), and the MoE expert shapes."""
+@pytest.mark.parametrize("K,N,gs", [
+    (320, 40, 32),     # general loop, ragged K (tail chunk) and N
+    (2048, 512, 64),   # persistent loop (the expert gate/up shape)
+    (1536, 200, 64),   # persistent loop, 3 steps per unit, ragged N
+    (2048, 512, 32),   # streaming loop (64 groups: past the persistent window)
+    (512, 2048, 64),   # general loop (the expert down shape)
+    (96, 16, 32)])
+def test_gather_qmm_shapes(dev, K, N, gs):
+    """Every gather main loop, ragged K and N, and the MoE expert shapes."""
     import torch
 
     from dflash_mlx_amd.moe import gather_qmm
 
-    gs = 32 if K % 64 else 64
     E, R, P = 6, 16, 24
     wq, s, b = _experts(E, N, K, gs, "bf16", seed=K + N)
     x = _x(R, K, "bf16", seed=3)
@@ -88,7 +93,7 @@ def test_gather_qmm_shapes(dev, K, N):
     _check(from_dev(got, "bf16"), want, "bf16")
 
 
-@pytest.mark.parametrize("K", [256, 1024])  # general and streaming main loops
+@pytest.mark.parametrize("K", [256, 1024])  # general and persistent main loops
 def test_gather_qmm_long_runs(dev, K):
     """Runs of more than 16 pairs on one expert (several MFMA row blocks), and
     lhs_indices=None (row p for pair p)."""
@@ -107,7 +112,7 @@ def test_gather_qmm_long_runs(dev, K):
     _check(from_dev(got, "bf16"), want, "bf16")
 
 
-@pytest.mark.parametrize("K", [256, 1024])  # general and streaming main loops
+@pytest.mark.parametrize("K", [256, 1024])  # general and persistent main loops
 def test_gather_qmm_invalid_ids_give_nan_rows(dev, K):
     import torch
 
