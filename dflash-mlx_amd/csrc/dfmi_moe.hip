@@ -298,28 +298,6 @@ struct PersistLayout {
   }
 };
 
-// s_waitcnt vmcnt(n) (n clamped to 15: waiting longer is safe) + barrier
-__device__ inline void persist_wait(int n) {
-  switch (n < 0 ? 0 : (n > 15 ? 15 : n)) {
-    case 0: stage_barrier<0>(); break;
-    case 1: stage_barrier<1>(); break;
-    case 2: stage_barrier<2>(); break;
-    case 3: stage_barrier<3>(); break;
-    case 4: stage_barrier<4>(); break;
-    case 5: stage_barrier<5>(); break;
-    case 6: stage_barrier<6>(); break;
-    case 7: stage_barrier<7>(); break;
-    case 8: stage_barrier<8>(); break;
-    case 9: stage_barrier<9>(); break;
-    case 10: stage_barrier<10>(); break;
-    case 11: stage_barrier<11>(); break;
-    case 12: stage_barrier<12>(); break;
-    case 13: stage_barrier<13>(); break;
-    case 14: stage_barrier<14>(); break;
-    default: stage_barrier<15>(); break;
-  }
-}
-
 template <typename Tag, int GS, bool GLU>
 __global__ __launch_bounds__(512) void gather_persist_kernel(GatherArgs a) {
   using LY = PersistLayout<Tag, GS>;
@@ -499,7 +477,7 @@ __global__ __launch_bounds__(512) void gather_persist_kernel(GatherArgs a) {
   // unit's window precedes its first chunk).
   auto wait_chunk = [&](int v) __attribute__((always_inline)) {
     const int upto = (v + 1) * S::CHUNK_DMA + (v / C + 1) * S::SB_DMA;  // loads up to chunk v
-    persist_wait(ops - upto);
+    stage_barrier_n(ops - upto);
   };
   auto read = [&](int v, typename S::Frag& f) __attribute__((always_inline)) {
     typename S::Ctx cr;  // what the fragment reads use: the wave and the unit's window

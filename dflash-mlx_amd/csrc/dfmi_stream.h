@@ -72,6 +72,29 @@ __device__ inline void stage_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// stage_barrier<n> for a runtime n (clamped to 15: waiting longer is safe)
+__device__ inline void stage_barrier_n(int n) {
+  switch (n < 0 ? 0 : (n > 15 ? 15 : n)) {
+    case 0: stage_barrier<0>(); break;
+    case 1: stage_barrier<1>(); break;
+    case 2: stage_barrier<2>(); break;
+    case 3: stage_barrier<3>(); break;
+    case 4: stage_barrier<4>(); break;
+    case 5: stage_barrier<5>(); break;
+    case 6: stage_barrier<6>(); break;
+    case 7: stage_barrier<7>(); break;
+    case 8: stage_barrier<8>(); break;
+    case 9: stage_barrier<9>(); break;
+    case 10: stage_barrier<10>(); break;
+    case 11: stage_barrier<11>(); break;
+    case 12: stage_barrier<12>(); break;
+    case 13: stage_barrier<13>(); break;
+    case 14: stage_barrier<14>(); break;
+    default: stage_barrier<15>(); break;
+  }
+}
+
+
 // Dynamic LDS of the streaming kernels (one allocation per workgroup).
 extern __shared__ __attribute__((aligned(16))) char dfmi_smem[];
 

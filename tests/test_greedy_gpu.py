@@ -110,7 +110,8 @@ def _lm_case(M, K, V, gs, seed, dtype="bf16"):
                                             (4, 1024, 5003, 32, "f16"), (32, 768, 2048, 128, "bf16"),
                                             (1, 256, 129, 64, "bf16"), (16, 1088, 4099, 64, "bf16"),
                                             (32, 1024, 3001, 64, "bf16"), (24, 2048, 777, 128, "f16"),
-                                            (16, 5120, 20000, 64, "bf16")])
+                                            (16, 5120, 20000, 64, "bf16"), (16, 2048, 777, 64, "bf16"),
+                                            (12, 4096, 9000, 128, "f16")])
 def test_lmhead_fused_matches_oracle(dev, M, K, V, gs, dtype):
     import torch
 
@@ -143,7 +144,7 @@ def test_lmhead_fused_matches_oracle(dev, M, K, V, gs, dtype):
     assert int(res2.accept_len.item()) == a and int(res2.bonus.item()) == bonus
 
 
-@pytest.mark.parametrize("K", [256, 512])  # general and streaming main loops
+@pytest.mark.parametrize("K", [256, 512, 2048])  # general and streaming main loops, 4 K steps
 def test_lmhead_exact_ties_pick_lowest_index(dev, K):
     from dflash_mlx_amd.lm_head import lm_head_greedy_accept
 
@@ -196,11 +197,12 @@ def test_lmhead_mask_and_softcap(dev):
     assert torch.equal(capped.posterior, sampling.greedy_tokens_with_mask(capped.logits, mask))
 
 
-def test_lmhead_repeatable_and_workspace_clean(dev):
+@pytest.mark.parametrize("K", [1024, 2048])  # streaming main loop, 2 and 4 K steps
+def test_lmhead_repeatable_and_workspace_clean(dev, K):
     from dflash_mlx_amd import sampling
     from dflash_mlx_amd.lm_head import lm_head_greedy_accept
 
-    M, K, V, gs = 16, 1024, 10007, 64
+    M, V, gs = 16, 10007, 64
     x, w_q, s, b = _lm_case(M, K, V, gs, seed=5)
     args = (to_dev(x, "bf16", dev), to_dev(w_q, "u32", dev), to_dev(s, "bf16", dev),
             to_dev(b, "bf16", dev))
