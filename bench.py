@@ -43,6 +43,8 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 METRIC = "M=16 int4 verify_qmm µs/call + achieved HBM GB/s (% of peak), 1 GPU"
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+MFMA_FILE = os.path.join(ROOT, "profiles", "mfma.json")
+MFMA_PEAK_TFLOPS = 2500.0  # dense bf16 MFMA, MI355X
 
 SHAPES_9B = [("q", 4096, 4096), ("k", 4096, 1024), ("v", 4096, 1024), ("o", 4096, 4096),
              ("gate", 4096, 12288), ("up", 4096, 12288), ("down", 12288, 4096)]
@@ -152,6 +154,22 @@ def measured_traffic(workload, kernel):
     return entry.get("bytes_per_launch")
 
 
+def mfma_report(workload, kernel, flops, us):
+    """MFMA side of a launch: algorithmic FLOP (2·rows·K·N) over its measured
+    time against the dense bf16 peak, and the MFMA-busy share that the
+    committed rocprofv3 counter pass recorded for the kernel (None if absent)."""
+    tflops = flops / (us * 1e-6) / 1e12
+    util = None
+    try:
+        with open(MFMA_FILE) as f:
+            util = json.load(f).get(workload, {}).get(kernel, {}).get("util_pct")
+    except (OSError, ValueError):
+        pass
+    return {"flops_per_launch": int(flops), "achieved_tflops": round(tflops, 2),
+            "peak_tflops": MFMA_PEAK_TFLOPS, "frac": round(tflops / MFMA_PEAK_TFLOPS, 5),
+            "busy_pct_counter": util}
+
+
 def base_result(args, value, ms, n_calls, config, roofline):
     return {
         "metric": METRIC,
@@ -252,6 +270,8 @@ def run_sweep(args, torch):
         per_kernel[name] = {"launches_per_step": len(subset), "ms_per_step": round(kms, 4),
                             "us_per_launch": round(kms * 1e3 / len(subset), 3),
                             "bytes_per_launch": kbytes // len(subset),
+                            "flops_per_launch": sum(2 * M * x.shape[1] * w.shape[0]
+                                                    for (x, w, _, _, _) in subset) // len(subset),
                             "GBps": round(kbytes / (kms * 1e-3) / 1e9, 2)}
     dom = max(per_kernel, key=lambda k: per_kernel[k]["ms_per_step"])
     d = per_kernel[dom]
@@ -260,6 +280,8 @@ def run_sweep(args, torch):
                 "traffic": measured_traffic(args.workload, dom),
                 "kernel": dom, "bytes_per_launch": d["bytes_per_launch"],
                 "us_per_launch": d["us_per_launch"], "per_kernel": per_kernel}
+    roofline["mfma"] = mfma_report(args.workload + ("_bits8" if bits == 8 else ""), dom,
+                                   d["flops_per_launch"], d["us_per_launch"])
     config = {"workload": f"{args.workload}-class dense verify-linear sweep",
               "layers": layers, "linears_per_layer": len(shapes), "M": M, "group_size": 64,
               "bits": bits, "launch": "eager" if args.no_graph else "hip-graph",
@@ -302,6 +324,7 @@ def run_single(args, torch):
     roofline = {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic("single", name),
                 "kernel": name, "bytes_per_launch": alg_bytes(M, K, N), "us_per_launch": round(us, 3)}
+    roofline["mfma"] = mfma_report("single", name, 2 * M * K * N, us)
     config = {"workload": "single call [16,4096]x[4096,4096] int4 gs64, weights rotated over "
                           f"{R} copies (1 GB)", "M": M, "K": K, "N": N}
     return base_result(args, gbs, ms, R, config, roofline)
@@ -346,6 +369,7 @@ def run_lmhead(args, torch):
                 "traffic": measured_traffic("lmhead", "lmhead_stream_kernel"),
                 "kernel": "lmhead_stream_kernel", "bytes_per_launch": nbytes,
                 "us_per_launch": round(ms * 1e3, 3)}
+    roofline["mfma"] = mfma_report("lmhead", "lmhead_stream_kernel", 2 * M * K * V, ms * 1e3)
     config = {"workload": "fused lm_head [16,5120]x[151936,5120] int4 gs64 + greedy + accept",
               "M": M, "K": K, "V": V, "calls_per_step": R}
     return base_result(args, gbs, ms_step, R, config, roofline)
@@ -435,6 +459,9 @@ def run_moe(args, torch):
                 "traffic": measured_traffic("moe", "gather_persist_kernel"),
                 "kernel": "gather_persist_kernel", "bytes_per_launch": dom["bytes_per_launch"],
                 "us_per_launch": dom["us_per_launch"], "per_kernel": per_kernel}
+    # algorithmic FLOP of the gate/up launch: T·k routed rows x (gate + up)
+    roofline["mfma"] = mfma_report("moe", "gather_persist_kernel", 2 * T * k * D * I * 2,
+                                   dom["us_per_launch"])
     config = {"workload": "MoE 40 layers, 16 tokens top-8 of 256 experts, hidden 2048, "
                           "expert width 512, int4 gs64", "algorithmic_bytes_per_step": total}
     return base_result(args, gbs, ms, 3 * layers, config, roofline)
