@@ -31,6 +31,10 @@ CFLAGS = [
     # MFMA results in VGPRs: the per-group scale FMAs read them directly
     # instead of copying each accumulator out of an AGPR first.
     "-mllvm", "-amdgpu-mfma-vgpr-form=1",
+    # Scalar kernel arguments arrive in SGPRs at wave start instead of
+    # through a scalar load from the kernarg segment (by-value structs are
+    # not preloaded; the streaming matmul takes its arguments as scalars).
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
 ]
 
 

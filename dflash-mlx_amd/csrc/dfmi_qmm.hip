@@ -159,7 +159,7 @@ struct StreamArgs {
 };
 
 template <typename Tag, int GS, int MT, int WV, int BITS, int SBPC>
-__global__ __launch_bounds__(64 * WV) void qmm_stream_kernel(StreamArgs a) {
+__device__ __forceinline__ void qmm_stream_body(StreamArgs a) {
   using S = Stream<Tag, GS, MT, WV, SBPC, BITS>;
   constexpr int kThreads = 64 * WV;
   int nb, kpi;
@@ -338,12 +338,24 @@ static int plan_stream(int64_t M, int64_t K, int64_t N, int gs, int bits,
   return DFMI_OK;
 }
 
+// The arguments as scalars, not a by-value struct, so that they are
+// preloaded into SGPRs at wave start (-amdgpu-kernarg-preload-count).
+template <typename Tag, int GS, int MT, int WV, int BITS, int SBPC>
+__global__ __launch_bounds__(64 * WV) void qmm_stream_kernel(
+    const uint16_t* x, const uint32_t* w, const uint16_t* s, const uint16_t* b, uint16_t* y,
+    float* partials, uint32_t* counters, int M, int K, int N, int chunks, int kp, int n_blocks,
+    int xcd_map) {
+  qmm_stream_body<Tag, GS, MT, WV, BITS, SBPC>(
+      StreamArgs{x, w, s, b, y, partials, counters, M, K, N, chunks, kp, n_blocks, xcd_map});
+}
+
 template <typename Tag, int GS, int MT, int WV, int BITS>
 static void launch_stream_t(const StreamPlan& p, hipStream_t st, const StreamArgs& a) {
   constexpr int SBPC = BITS == 8 && WV == 8 ? 8 : kSbPieces;  // = stream_sb_pieces(BITS, WV)
   const int lds = Stream<Tag, GS, MT, WV, SBPC, BITS>::LDS_BYTES;
   hipLaunchKernelGGL((qmm_stream_kernel<Tag, GS, MT, WV, BITS, SBPC>), dim3(p.grid_x),
-                     dim3(64 * WV), lds, st, a);
+                     dim3(64 * WV), lds, st, a.x, a.w, a.s, a.b, a.y, a.partials, a.counters,
+                     a.M, a.K, a.N, a.chunks, a.kp, a.n_blocks, a.xcd_map);
 }
 
 template <typename Tag, int GS, int BITS>
