@@ -652,7 +652,8 @@ static int validate_gather(int x_dtype, int64_t x_rows, int64_t P, int64_t K, in
     set_error("dfmi_gather_qmm: group_size=%d unsupported (32, 64, 128)", gs);
     return DFMI_EINVAL;
   }
-  if (P < 0 || N < 0 || E < 1 || x_rows < 1 || K < 32 || K % 32 || K % gs) {
+  // no pairs (zero tokens routed) needs no activation rows
+  if (P < 0 || N < 0 || E < 1 || x_rows < (P > 0 ? 1 : 0) || K < 32 || K % 32 || K % gs) {
     set_error("dfmi_gather_qmm: bad shape P=%lld K=%lld N=%lld E=%lld x_rows=%lld gs=%d",
               (long long)P, (long long)K, (long long)N, (long long)E, (long long)x_rows, gs);
     return DFMI_EINVAL;

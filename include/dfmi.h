@@ -123,6 +123,7 @@ size_t dfmi_qmm_workspace_bytes_ex(int64_t M, int64_t K, int64_t N, int group_si
  * per pair.  Expert ids outside [0, E) and row ids outside [0, x_rows) are
  * checked on the device: that pair's output row is filled with NaN (the call
  * still returns DFMI_OK; validate on the host when it matters).  P <= 65535.
+ * P == 0 (or N == 0) is a no-op, and then x_rows may be 0.
  */
 int dfmi_gather_qmm_affine(const void *x, int x_dtype, int64_t x_rows, const uint32_t *w_q,
                            const void *scales, const void *biases, const int32_t *lhs_rows,

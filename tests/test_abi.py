@@ -70,6 +70,12 @@ def test_host_side_validation_without_gpu(lib):
     assert lib.dfmi_gather_qmm_affine(None, _lib.DFMI_BF16, 4, None, None, None, None, None, None,
                                       8, 256, 64, 4, 64, 8, None) == _lib.DFMI_EINVAL
     assert lib.dfmi_moe_combine(None, _lib.DFMI_F32, None, None, None, 4, 2, 8, None) == _lib.DFMI_EINVAL
+    # no routed pairs (zero tokens, so no activation rows either) and no tokens are no-ops
+    assert lib.dfmi_gather_qmm_affine(None, _lib.DFMI_BF16, 0, None, None, None, None, None, None,
+                                      0, 256, 64, 4, 64, 4, None) == _lib.DFMI_OK
+    assert lib.dfmi_gather_qmm_affine(None, _lib.DFMI_BF16, 0, None, None, None, None, None, None,
+                                      3, 256, 64, 4, 64, 4, None) == _lib.DFMI_EINVAL
+    assert lib.dfmi_moe_combine(None, _lib.DFMI_BF16, None, None, None, 0, 2, 8, None) == _lib.DFMI_OK
     # GDN pair: Dk must be 32 * {1, 2, 4, 8, 16}, Hv a multiple of Hk, float dtypes
     bf, f32 = _lib.DFMI_BF16, _lib.DFMI_F32
     gdn = [None] * 10

@@ -207,3 +207,23 @@ def test_moe_combine_unsort(dev, T, k, D):
     assert np.isnan(out[T - 1]).all()
     assert np.array_equal(from_dev(moe_combine(y_sorted, scd, y_rows=bad), "bf16")[: T - 1],
                           got[: T - 1])
+
+
+def test_empty_calls(dev):
+    """Zero tokens: no pairs, no activation rows; every MoE operator returns
+    empty results without a launch."""
+    import torch
+
+    from dflash_mlx_amd.moe import gather_qmm, gather_swiglu, moe_combine
+
+    E, N, K = 3, 32, 256
+    wq, s, b = _experts(E, N, K, 64, "bf16", seed=1)
+    tr = (to_dev(wq, "u32", dev), to_dev(s, "bf16", dev), to_dev(b, "bf16", dev))
+    x = torch.empty((0, K), dtype=torch.bfloat16, device=dev)
+    rhs = torch.empty((0,), dtype=torch.int32, device=dev)
+    assert tuple(gather_qmm(x, *tr, rhs, group_size=64).shape) == (0, N)
+    assert tuple(gather_swiglu(x, tr, tr, rhs, group_size=64).shape) == (0, N)
+    y = torch.empty((0, N), dtype=torch.bfloat16, device=dev)
+    sc = torch.empty((0, 2), dtype=torch.float32, device=dev)
+    assert tuple(moe_combine(y, sc).shape) == (0, N)
+    torch.cuda.synchronize()

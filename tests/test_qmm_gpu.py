@@ -288,3 +288,22 @@ def test_captured_graph_survives_workspace_growth(dev):
         _, rel = oracle.parity_metrics(oracle.to_f32(from_dev(yg, "bf16"), "bf16"), want)
         assert rel <= REL_TOL
     assert all(bool((f == 7).all()) for f in fills)
+
+
+def test_empty_rows(dev):
+    """x with no rows gives an empty [.., N] result through both Python entry
+    points, without a launch."""
+    import torch
+
+    from dflash_mlx_amd.verify_qmm import quantized_matmul, verify_matmul
+
+    K, N = 512, 96
+    w = (np.random.default_rng(3).standard_normal((N, K)) * 0.02).astype(np.float32)
+    q, s, b = oracle.quantize(w, 64, 4, out_dtype="bf16")
+    args = (to_dev(q, "u32", dev), to_dev(s, "bf16", dev), to_dev(b, "bf16", dev))
+    for fn in (quantized_matmul, verify_matmul):
+        for shape in ((0, K), (2, 0, K)):
+            x = torch.empty(shape, dtype=torch.bfloat16, device=dev)
+            y = fn(x, *args, group_size=64, bits=4)
+            assert tuple(y.shape) == shape[:-1] + (N,)
+    torch.cuda.synchronize()
