@@ -135,7 +135,8 @@ def test_gather_qmm_invalid_ids_give_nan_rows(dev, K):
 
 
 @pytest.mark.parametrize("T,k,E,D,I", [(4, 2, 8, 256, 128), (16, 8, 32, 2048, 512),
-                                       (5, 3, 6, 1024, 192)])
+                                       (5, 3, 6, 1024, 192),
+                                       (16, 8, 128, 1024, 256)])  # ~1 routed row per expert
 def test_switch_glu_matches_oracle(dev, T, k, E, D, I):
     import torch
 

@@ -64,6 +64,15 @@ def test_baseline_layer_shapes_m16(dev, K, N):
     _check(_run(dev, x, w_q, s, b, 64), x, w_q, s, b, 64)
 
 
+@pytest.mark.parametrize("M", [4, 8, 32])
+@pytest.mark.parametrize("K,N", [(4096, 12288), (4096, 1024), (17408, 5120), (5120, 17408)])
+def test_layer_shapes_other_m(dev, M, K, N):
+    """The adaptive M=4 block and the 27B sweep's M=8 / M=32 on the layer
+    shapes they run at."""
+    x, w_q, s, b = make_qmm_case(M, K, N, 64, seed=K + N + M)
+    _check(_run(dev, x, w_q, s, b, 64), x, w_q, s, b, 64)
+
+
 @pytest.mark.parametrize("M", [1, 4, 8, 12, 15, 17, 24, 32, 48, 80])
 def test_m_sweep(dev, M):
     x, w_q, s, b = make_qmm_case(M, 2048, 768, 64, seed=100 + M)
