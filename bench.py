@@ -556,7 +556,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU only (--gpus 1); how the path "
+        print(json.dumps({"error": "bench.py measures one GPU only (--gpus 1); how the path "
                                    "shards over several GPUs is a design note, not a run"}))
         sys.exit(2)
     import torch

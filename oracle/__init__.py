@@ -2,7 +2,7 @@
 
 This package restates, in plain numpy, the arithmetic that the reference
 (shaneholloman/dflash-mlx 0.1.7) and the MLX operators it calls perform on the
-verify path.  It is the checker for the HIP kernels: only ``tests/``,
+verify path.  It is the reference the HIP kernels are tested against: only ``tests/``,
 ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg may import
 it, and never as the thing measured or shipped.  The product package must not
 import it.
