@@ -15,8 +15,10 @@ bf16 scales/biases + x + y), us_per_call, the HBM roofline of the dominant
 kernel (its launches replayed alone and timed with HIP events on the stream
 they run on; ``traffic`` = measured HBM bytes per launch from the rocprofv3
 FETCH_SIZE / WRITE_SIZE summary in profiles/, when one exists for this
-workload and kernel) and a CPU baseline (the oracle's C restatement on this
-host's cores, on a bounded sample: layer 0's seven matmuls).
+workload and kernel; ``mfma`` = its algorithmic TFLOP/s against the dense
+bf16 peak and the MFMA-busy share from the rocprofv3 counter summary) and a
+CPU baseline (the oracle's C restatement on this host's cores, on a bounded
+sample: layer 0's seven matmuls).
 
 Other workloads (``--workload``, not the default line): ``27b`` (64 layers,
 hidden 5120, ``--m`` 8/16/32), ``single`` ([16,4096]x[4096,4096], weights
