@@ -319,6 +319,12 @@ static int plan_stream(int64_t M, int64_t K, int64_t N, int gs, int bits,
     // (every split pays a pipeline fill and the partial-sum epilogue)
     kp = (int)std::lround(256.0 / (double)p.n_blocks);
     kp = std::max(1, std::min(kp, (int)(K / 1024)));
+    // two 4-bit activation blocks: two 80 KB workgroups share a CU, so up to
+    // 512 workgroups run at once; raise the split toward that while every
+    // split keeps at least 8 steps (27B-class down projection at M = 32:
+    // 6 splits 21.5 us vs 3 splits 25.2 us)
+    if (p.MT == 2 && bits == 4)
+      kp = std::max(kp, std::min(512 / p.n_blocks, (int)(K / 2048)));
   }
   p.kp = std::max(1, std::min(kp, (int)(K / 256)));
   if (p.n_blocks > kMaxCounters) p.kp = 1;
