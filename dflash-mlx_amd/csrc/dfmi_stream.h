@@ -140,10 +140,11 @@ struct Stream {
   // measured slower than three on MI355X (4096x12288: 12.8 us vs 11.4 us):
   // the extra step in flight does not raise the per-CU request rate, and the
   // longer wait chain delays the first MFMA.  Two activation blocks (MT = 2)
-  // take two stages: 80 KB with 4-bit weights, so two workgroups share a CU
+  // with 4-bit weights take two stages: 80 KB, so two workgroups share a CU
   // and each one's wait is the other's compute (27B-class sweep at M = 32:
-  // 7.59 ms vs 8.28 ms with three stages and one workgroup per CU).
-  static constexpr int DEPTH = MT == 2 ? 2 : 3;
+  // 7.59 ms vs 8.28 ms with three stages and one workgroup per CU).  8-bit
+  // stages would still need 96 KB, one workgroup per CU: they keep three.
+  static constexpr int DEPTH = MT == 2 && BITS == 4 ? 2 : 3;
   // gs >= 64: a lane's two k-blocks take adjacent words (one 8-byte LDS read);
   // gs = 32: k-block j is group 2*wave + j, so the blocks stay group-pure.
   static constexpr bool PAIR = GS >= 64;
