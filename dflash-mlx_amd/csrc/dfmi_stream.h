@@ -143,8 +143,11 @@ struct Stream {
   // with 4-bit weights take two stages: 80 KB, so two workgroups share a CU
   // and each one's wait is the other's compute (27B-class sweep at M = 32:
   // 7.59 ms vs 8.28 ms with three stages and one workgroup per CU).  8-bit
-  // stages would still need 96 KB, one workgroup per CU: they keep three.
-  static constexpr int DEPTH = MT == 2 && BITS == 4 ? 2 : 3;
+  // weights with one activation block and 4 wavefronts likewise fit 80 KB in
+  // two stages; with two blocks they would still need 96 KB (one workgroup
+  // per CU), so they keep three.
+  static constexpr int DEPTH =
+      (MT == 2 && BITS == 4) || (MT == 1 && BITS == 8 && WV == 4) ? 2 : 3;
   // gs >= 64: a lane's two k-blocks take adjacent words (one 8-byte LDS read);
   // gs = 32: k-block j is group 2*wave + j, so the blocks stay group-pure.
   static constexpr bool PAIR = GS >= 64;
