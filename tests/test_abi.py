@@ -98,3 +98,28 @@ def test_workspace_queries(lib):
     assert lib.dfmi_qmm_workspace_bytes(16, 4096, 4096, 64, 3) == 0
     assert lib.dfmi_greedy_workspace_bytes(16) >= 256 + 8 * 16
     assert lib.dfmi_lmhead_workspace_bytes(16) >= 256 + 8 * 16
+
+
+def test_streaming_split_plans(lib):
+    """The streaming matmul's K-split plan, read back through the workspace
+    query (65536 counter bytes + kp fp32 partials of [M, N] when kp > 1)."""
+    def splits(M, K, N, bits):
+        ws = lib.dfmi_qmm_workspace_bytes(M, K, N, 64, bits)
+        if ws == 0:
+            return 1
+        kp, rem = divmod(ws - 65536, M * N * 4)
+        assert rem == 0, ws
+        return kp
+
+    # M = 16, 4-bit: one 8-wavefront workgroup per CU, ~256 workgroups
+    assert splits(16, 4096, 4096, 4) == 4
+    assert splits(16, 12288, 4096, 4) == 4
+    assert splits(16, 4096, 12288, 4) == 1
+    # M = 17..32, 4-bit: two workgroups per CU, splits toward 512 workgroups
+    # while each split keeps >= 8 steps of 256 k
+    assert splits(32, 17408, 5120, 4) == 6
+    assert splits(32, 5120, 5120, 4) == 3
+    assert splits(32, 5120, 17408, 4) == 1
+    # 8-bit, M = 16: the unsplit 192-block grid runs as 4 wavefronts, 2 splits
+    assert splits(16, 4096, 12288, 8) == 2
+    assert splits(16, 4096, 4096, 8) == 4
