@@ -11,7 +11,6 @@
 #include <cmath>
 
 #include "dfmi_core.h"
-#include "dfmi_direct.h"
 #include "dfmi_host.h"
 #include "dfmi_stream.h"
 
@@ -430,118 +429,6 @@ static void allow_lds_all() {
   (void)done;
 }
 
-// ---------------------------------------------------------------------------
-// Register-direct path (Direct main loop): M <= 16, K % 256 == 0.  A
-// workgroup of KW wavefronts owns 16*NT weight rows; the wavefronts split the
-// K steps between them and sum their partial tiles through LDS, so every
-// output element is written once, with no atomics and no workspace.
-
-struct DirectArgs {
-  const uint16_t* x;
-  const uint32_t* w;
-  const uint16_t* s;
-  const uint16_t* b;
-  uint16_t* y;
-  int M, K, N;
-};
-
-template <typename Tag, int GS, int NT>
-__global__ __launch_bounds__(kDirectMaxWaves * 64) void qmm_direct_kernel(DirectArgs a) {
-  using D = Direct<Tag, GS, NT>;
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int waves = blockDim.x >> 6;
-  const int n0 = blockIdx.x * 16 * NT;
-  const typename D::Ctx c = D::setup(a.x, a.w, a.s, a.b, a.M, a.K, a.N, n0, lane);
-  const int steps = a.K / kDirectK;
-  const int i0 = wave * steps / waves, i1 = (wave + 1) * steps / waves;
-  f32x4 acc[NT];
-#pragma unroll
-  for (int t = 0; t < NT; ++t) acc[t] = zero4();
-  if (i1 > i0) D::run(c, i0, i1, acc, lane);
-  if (waves == 1) {
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = 4 * (lane >> 4) + r, n = n0 + 16 * t + (lane & 15);
-        if (m < a.M && n < a.N) a.y[(int64_t)m * a.N + n] = Num<Tag>::f2h(acc[t][r]);
-      }
-    return;
-  }
-  float* red = reinterpret_cast<float*>(dfmi_smem);
-  {
-    float* mine = red + wave * D::RED_FLOATS;
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) mine[(t * 4 + r) * 64 + lane] = acc[t][r];
-  }
-  __syncthreads();
-  for (int e = threadIdx.x; e < D::RED_FLOATS; e += blockDim.x) {
-    float v = red[e];
-    for (int wv = 1; wv < waves; ++wv) v += red[wv * D::RED_FLOATS + e];
-    const int l = e & 63, r = (e >> 6) & 3, t = e >> 8;
-    const int m = 4 * (l >> 4) + r, n = n0 + 16 * t + (l & 15);
-    if (m < a.M && n < a.N) a.y[(int64_t)m * a.N + n] = Num<Tag>::f2h(v);
-  }
-}
-
-struct DirectPlan {
-  int NT, KW, grid, lds;
-};
-
-// (buffer offsets are 32-bit: every operand stays under 2 GiB)
-static bool direct_eligible(int64_t M, int64_t K, int64_t N, int gs) {
-  return M <= 16 && K % kDirectK == 0 && M * K * 2 < (1ll << 31) && N * (K / 2) < (1ll << 31) &&
-         N * (K / gs) * 2 < (1ll << 31);
-}
-
-static int plan_direct(int64_t M, int64_t K, int64_t N, const dfmi_qmm_tuning* tune,
-                       DirectPlan& p) {
-  (void)M;
-  const int64_t tiles = (N + 15) / 16;
-  int nt = (tune && tune->tiles_per_wave) ? tune->tiles_per_wave : (tiles <= 1024 ? 1 : 2);
-  if (nt != 1 && nt != 2 && nt != 4) {
-    set_error("dfmi_qmm: tiles_per_wave must be 1, 2 or 4 (got %d)", nt);
-    return DFMI_EINVAL;
-  }
-  const int64_t grid = (tiles + nt - 1) / nt;
-  const int steps = (int)(K / kDirectK);
-  int kw;
-  if (tune && tune->waves_per_block) {
-    kw = tune->waves_per_block;
-    if (kw < 1 || kw > kDirectMaxWaves) {
-      set_error("dfmi_qmm: waves_per_block must be 1..%d (got %d)", kDirectMaxWaves, kw);
-      return DFMI_EINVAL;
-    }
-  } else {
-    // about 3072 wavefronts in flight (3 per SIMD), each with >= 2 steps
-    kw = (int)std::max<int64_t>(1, std::min<int64_t>(kDirectMaxWaves, 3072 / std::max<int64_t>(1, grid)));
-    kw = std::max(1, std::min(kw, steps / 2));
-  }
-  p.NT = nt;
-  p.KW = std::max(1, std::min(kw, steps));
-  p.grid = (int)grid;
-  p.lds = p.KW > 1 ? p.KW * nt * 1024 : 0;
-  return DFMI_OK;
-}
-
-template <typename Tag, int GS>
-static void launch_direct_gs(const DirectPlan& p, hipStream_t st, const DirectArgs& a) {
-  const dim3 g(p.grid), blk(64 * p.KW);
-  if (p.NT == 1) hipLaunchKernelGGL((qmm_direct_kernel<Tag, GS, 1>), g, blk, p.lds, st, a);
-  else if (p.NT == 2) hipLaunchKernelGGL((qmm_direct_kernel<Tag, GS, 2>), g, blk, p.lds, st, a);
-  else hipLaunchKernelGGL((qmm_direct_kernel<Tag, GS, 4>), g, blk, p.lds, st, a);
-}
-
-template <typename Tag>
-static void launch_direct(int gs, const DirectPlan& p, hipStream_t st, const DirectArgs& a) {
-  if (gs == 32) launch_direct_gs<Tag, 32>(p, st, a);
-  else if (gs == 64) launch_direct_gs<Tag, 64>(p, st, a);
-  else launch_direct_gs<Tag, 128>(p, st, a);
-}
-
 static int validate_qmm(int x_dtype, int64_t M, int64_t K, int64_t N, int gs, int bits) {
   if (x_dtype != DFMI_BF16 && x_dtype != DFMI_F16) {
     set_error("dfmi_qmm: x dtype %d unsupported (bf16 or f16)", x_dtype);
@@ -576,17 +463,11 @@ using namespace dfmi;
 // Automatic choice (measured on MI355X): the streaming kernel is faster on
 // every shape it takes; the general kernel covers the rest (M > 32, K not a
 // multiple of 256 or of 8 groups, weights over 2 GiB).
-static bool use_direct(int64_t M, int64_t K, int64_t N, int gs, int bits,
-                       const dfmi_qmm_tuning* tune) {
-  const int path = tune ? tune->path : 0;
-  return bits == 4 && path == 3 && direct_eligible(M, K, N, gs);
-}
-
 static bool use_stream(int64_t M, int64_t K, int64_t N, int gs, int bits,
                        const dfmi_qmm_tuning* tune) {
   const int path = tune ? tune->path : 0;
   if (bits != 4 && bits != 8) return false;
-  if (path == 1 || path == 3) return false;
+  if (path == 1) return false;
   // more blocks than split counters run unsplit: the whole K in one scale
   // window (8-bit: the smaller window of its plans)
   const int sbpc = bits == 8 ? 8 : kSbPieces;
@@ -594,9 +475,15 @@ static bool use_stream(int64_t M, int64_t K, int64_t N, int gs, int bits,
          ((N + kStreamRows - 1) / kStreamRows <= kMaxCounters || K / gs <= sb_max_groups(sbpc));
 }
 
+// tuning.path: 0 automatic, 1 general kernel, 2 streaming kernel
+static bool valid_path(const dfmi_qmm_tuning* tune) {
+  return !tune || (tune->path >= 0 && tune->path <= 2);
+}
+
 extern "C" size_t dfmi_qmm_workspace_bytes_ex(int64_t M, int64_t K, int64_t N, int group_size,
                                               int bits, const dfmi_qmm_tuning* tuning) {
-  if (validate_qmm(DFMI_BF16, M, K, N, group_size, bits) != DFMI_OK || M == 0 || N == 0)
+  if (validate_qmm(DFMI_BF16, M, K, N, group_size, bits) != DFMI_OK || M == 0 || N == 0 ||
+      !valid_path(tuning))
     return 0;
   if (!use_stream(M, K, N, group_size, bits, tuning)) return 0;
   StreamPlan p;
@@ -606,10 +493,10 @@ extern "C" size_t dfmi_qmm_workspace_bytes_ex(int64_t M, int64_t K, int64_t N, i
 
 extern "C" const char* dfmi_qmm_kernel_name(int64_t M, int64_t K, int64_t N, int group_size,
                                              int bits, const dfmi_qmm_tuning* tuning) {
-  if (validate_qmm(DFMI_BF16, M, K, N, group_size, bits) != DFMI_OK) return nullptr;
+  if (validate_qmm(DFMI_BF16, M, K, N, group_size, bits) != DFMI_OK || !valid_path(tuning))
+    return nullptr;
   if (bits == 8) return use_stream(M, K, N, group_size, bits, tuning) ? "qmm8_stream_kernel"
                                                                       : "qmm8_kernel";
-  if (use_direct(M, K, N, group_size, bits, tuning)) return "qmm_direct_kernel";
   return use_stream(M, K, N, group_size, bits, tuning) ? "qmm_stream_kernel" : "qmm_dense_kernel";
 }
 
@@ -625,7 +512,19 @@ extern "C" int dfmi_qmm_affine_ex(const void* x, int x_dtype, const uint32_t* w_
                                   void* stream) {
   int rc = validate_qmm(x_dtype, M, K, N, group_size, bits);
   if (rc != DFMI_OK) return rc;
+  if (!valid_path(tuning)) {
+    set_error("dfmi_qmm: tuning path %d unsupported (0 auto, 1 general, 2 streaming)",
+              tuning->path);
+    return DFMI_EINVAL;
+  }
   if (M == 0 || N == 0) return DFMI_OK;
+  // a forced streaming plan on a shape outside the streaming kernel is an
+  // error for both weight widths (checked before the 8-bit fallback)
+  if (tuning && tuning->path == 2 && !use_stream(M, K, N, group_size, bits, tuning)) {
+    set_error("dfmi_qmm: shape M=%lld K=%lld N=%lld gs=%d bits=%d outside the streaming kernel",
+              (long long)M, (long long)K, (long long)N, group_size, bits);
+    return DFMI_EINVAL;
+  }
   if (!x || !w_q || !scales || !biases || !y) {
     set_error("dfmi_qmm: null pointer");
     return DFMI_EINVAL;
@@ -638,33 +537,6 @@ extern "C" int dfmi_qmm_affine_ex(const void* x, int x_dtype, const uint32_t* w_
   // 8-bit: the streaming kernel where it applies, else the register-load kernel
   if (bits == 8 && !use_stream(M, K, N, group_size, bits, tuning))
     return dfmi_qmm8_launch(x, x_dtype, w_q, scales, biases, y, M, K, N, group_size, stream);
-  if (tuning && tuning->path == 2 && !stream_eligible(M, K, N, group_size)) {
-    set_error("dfmi_qmm: shape M=%lld K=%lld gs=%d outside the streaming kernel", (long long)M,
-              (long long)K, group_size);
-    return DFMI_EINVAL;
-  }
-  if (tuning && tuning->path == 3 && !direct_eligible(M, K, N, group_size)) {
-    set_error("dfmi_qmm: shape M=%lld K=%lld gs=%d outside the register-direct kernel",
-              (long long)M, (long long)K, group_size);
-    return DFMI_EINVAL;
-  }
-  if (use_direct(M, K, N, group_size, bits, tuning)) {
-    DirectPlan p;
-    rc = plan_direct(M, K, N, tuning, p);
-    if (rc != DFMI_OK) return rc;
-    DirectArgs a;
-    a.x = static_cast<const uint16_t*>(x);
-    a.w = w_q;
-    a.s = static_cast<const uint16_t*>(scales);
-    a.b = static_cast<const uint16_t*>(biases);
-    a.y = static_cast<uint16_t*>(y);
-    a.M = (int)M;
-    a.K = (int)K;
-    a.N = (int)N;
-    if (x_dtype == DFMI_BF16) launch_direct<BF16>(group_size, p, st, a);
-    else launch_direct<F16>(group_size, p, st, a);
-    return check_launch("dfmi_qmm_affine");
-  }
   if (use_stream(M, K, N, group_size, bits, tuning)) {
     StreamPlan p;
     rc = plan_stream(M, K, N, group_size, bits, tuning, p);

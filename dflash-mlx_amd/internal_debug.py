@@ -1,3 +1,10 @@
+# The flag names, defaults and parsing in this file follow
+# dflash_mlx/internal_debug.py of dflash-mlx 0.1.7:
+#   Copyright 2026 bstnxbt
+#   Licensed under the Apache License, Version 2.0
+#   Based on DFlash (arXiv:2602.06036)
+# They are kept identical because users set these environment variables.
+
 """Kernel-debug flag surface (same names, defaults and parsing as
 dflash_mlx/internal_debug.py:10-37).  Read at call time, never cached."""
 

@@ -25,8 +25,7 @@ from .internal_debug import (
 )
 from .quantize import quantize
 from .verify_qmm import (
-    _auto_variant,
-    _tuning,
+    _kparts_tuning,
     _m4_ksplit_np_shape,
     _resolve_m16_ktmpl_variant,
     qmm_launch,
@@ -165,13 +164,11 @@ def _build_dispatch(obj: VerifyQuantizedLinear, *, enable_qmm: Optional[bool] = 
     ktmpl_variant = _resolve_m16_ktmpl_variant(K, N, bits) if qmm_enabled else None
     m16_qmm = qmm_enabled and (ktmpl_variant is not None or (N % 32 == 0 and K % 32 == 0))
     m4_qmm = qmm_enabled and _m4_ksplit_np_shape(K, N, bits)
-    m16_tuning = None
-    if m16_qmm and ktmpl_variant is None:
-        # Reference 176-188: auto variant; pipe needs K % (32*K_PARTS) == 0.
-        variant, k_parts = _auto_variant(K, N)
-        if variant == "mma2big_pipe" and K % (32 * k_parts) != 0:
-            variant, k_parts = "mma2big", 1
-        m16_tuning = _tuning(k_parts if variant == "mma2big_pipe" else 1)
+    # Reference 176-188 picks mma2big_pipe (K_PARTS 8) or mma2big for shapes
+    # the K-templated kernels decline; both run the automatic plan here (the
+    # K_PARTS values are Metal launch choices), or DFLASH_VERIFY_QMM_KPARTS
+    # splits when the user sets it.
+    m16_tuning = _kparts_tuning() if (m16_qmm and ktmpl_variant is None) else None
 
     def _stock(x):
         return quantized_matmul(x, obj.weight, obj.scales, obj.biases, transpose=True,

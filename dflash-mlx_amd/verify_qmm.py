@@ -5,11 +5,14 @@ predicates (21-51), ``_should_use_verify`` (886-903) and ``verify_matmul``
 (905-1022).  Every route -- the M=16 K-templated variants, the mma2big /
 mma2big_pipe variants, the M=4 k-split variant and the "stock" fallback that
 the reference hands to ``mx.quantized_matmul`` -- runs the same hand-written
-gfx950 kernel family in libdfmi.so (``dfmi_qmm_affine``).  The route only
-selects the launch shape: the reference's ``K_PARTS`` becomes the number of
-K splits (``DFLASH_VERIFY_QMM_KPARTS`` keeps its meaning), the others use the
-automatic shape.  All shapes compute the same sums in fp32 and
-differ only in fp32 summation order.
+gfx950 kernel family in libdfmi.so (``dfmi_qmm_affine``).  The route decides
+which calls take the verify path (the reference's admission rules, restated
+rule for rule); the launch shape is the library's automatic plan, unless
+``DFLASH_VERIFY_QMM_KPARTS`` is set, in which case that many workgroups split
+K (the meaning the reference gives it).  The reference's built-in K_PARTS
+defaults (8 for mma2big_pipe, 1 for mma2big) are Metal launch choices and are
+not forced on this GPU.  All shapes compute the same sums in fp32 and differ
+only in fp32 summation order.
 
 Tensors: ``x`` bf16/f16 ``[..., K]`` on the GPU; ``w`` int32/uint32 words
 ``[N, K*bits/32]``; ``scales``/``biases`` ``[N, K/group_size]`` in x's dtype.
@@ -19,6 +22,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+import os
 from typing import Optional
 
 import torch
@@ -83,13 +87,23 @@ def _resolve_m16_ktmpl_variant(K: int, N: int, bits: int,
 
 
 def _tuning(k_parts: int = 0):
-    """Launch-shape hint from the reference's K_PARTS: the number of K splits
+    """Launch-shape hint from a K_PARTS value: the number of K splits
     (workgroups on the streaming kernel, wavefronts on the general one, at
     most 8); 0 means automatic."""
     if not k_parts:
         return None
     kp = max(1, min(8, int(k_parts)))
     return _lib.QmmTuning(0, 0, kp, kp)
+
+
+def _kparts_tuning():
+    """The launch shape of an M=16 verify call: automatic, or the split count
+    ``DFLASH_VERIFY_QMM_KPARTS`` asks for when the user sets it."""
+    raw = os.environ.get("DFLASH_VERIFY_QMM_KPARTS")
+    if raw is None:
+        return None
+    kp = _debug_verify_qmm_kparts(0)
+    return _tuning(kp) if kp > 0 else None
 
 
 def qmm_launch(x2: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
@@ -179,10 +193,10 @@ def verify_route(M: int, K: int, N: int, bits: int,
     if selected == "mma2big_pipe":
         if N % 32 != 0 or k_parts <= 0 or K % (32 * k_parts) != 0:
             return "stock", None
-        return "mma2big_pipe", _tuning(k_parts)
+        return "mma2big_pipe", _kparts_tuning()
     if N % 32 != 0 or K % 32 != 0:
         return "stock", None
-    return "mma2big", _tuning(1)
+    return "mma2big", _kparts_tuning()
 
 
 def verify_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,

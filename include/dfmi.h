@@ -49,17 +49,13 @@ const char *dfmi_last_error(void);
 /* Optional launch-shape override for the affine qmm (tuning sweeps).  Zero
  * fields mean "automatic".
  *   path: 1 = general kernel, 2 = streaming kernel (DFMI_EINVAL if the shape
- *         is outside it: M <= 32, K % 256 == 0, K % (8*group_size) == 0),
- *         3 = register-direct kernel (DFMI_EINVAL outside M <= 16,
- *         K % 256 == 0; measured slower than the streaming kernel on every
- *         verify shape, kept for tuning sweeps);
+ *         is outside it: M <= 32, K % 256 == 0, K % (8*group_size) == 0;
+ *         checked for both weight widths); any other value is DFMI_EINVAL;
  *   tiles_per_wave: general kernel, 16-row weight tiles per wavefront (1, 2,
- *         4); register-direct kernel, tiles per workgroup (1, 2, 4); the
- *         streaming kernel always covers 64 rows per workgroup;
+ *         4); the streaming kernel always covers 64 rows per workgroup;
  *   waves_per_block: general kernel, wavefronts of a workgroup that split K
  *         (1..8; the reference's K_PARTS); streaming kernel, 4 or 8
- *         wavefronts (8 needs M <= 16 and K % 512 == 0); register-direct
- *         kernel, wavefronts that split K (1..8);
+ *         wavefronts (8 needs M <= 16 and K % 512 == 0);
  *   k_splits: streaming kernel, workgroups that split K of one output block
  *         (raised if a split's K range would exceed one scale / bias window
  *         of 120 groups). */

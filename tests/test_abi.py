@@ -67,6 +67,22 @@ def test_host_side_validation_without_gpu(lib):
     # empty problems are a no-op
     assert lib.dfmi_qmm_affine(None, _lib.DFMI_BF16, None, None, None, None, 0, 4096, 4096, 64, 4,
                                None, 0, None) == _lib.DFMI_OK
+    # a forced streaming plan outside the streaming kernel is an error for
+    # both weight widths (M > 32; K not whole 256-k steps), and so is an
+    # unknown path
+    for bits in (4, 8):
+        for (M, K) in ((40, 1024), (16, 96)):
+            t = _lib.QmmTuning(2, 0, 0, 0)
+            assert lib.dfmi_qmm_affine_ex(None, _lib.DFMI_BF16, None, None, None, None, M, K, 64,
+                                          32, bits, None, 0, ctypes.byref(t), None) \
+                == _lib.DFMI_EINVAL
+            assert b"outside the streaming kernel" in lib.dfmi_last_error()
+    for path in (3, -1):
+        t = _lib.QmmTuning(path, 0, 0, 0)
+        assert lib.dfmi_qmm_affine_ex(None, _lib.DFMI_BF16, None, None, None, None, 16, 4096,
+                                      4096, 64, 4, None, 0, ctypes.byref(t), None) \
+            == _lib.DFMI_EINVAL
+        assert lib.dfmi_qmm_kernel_name(16, 4096, 4096, 64, 4, ctypes.byref(t)) is None
     assert lib.dfmi_gather_qmm_affine(None, _lib.DFMI_BF16, 4, None, None, None, None, None, None,
                                       8, 256, 64, 4, 64, 8, None) == _lib.DFMI_EINVAL
     assert lib.dfmi_moe_combine(None, _lib.DFMI_F32, None, None, None, 4, 2, 8, None) == _lib.DFMI_EINVAL

@@ -62,6 +62,34 @@ def test_verify_route_fallbacks():
     assert verify_qmm.verify_route(16, 4128, 4112, 4)[0] == "stock"
 
 
+def test_verify_route_launch_shape(monkeypatch):
+    """The mma2big routes admit calls by the reference's rules but launch the
+    library's automatic plan (the reference's K_PARTS defaults are Metal
+    launch choices): 8-bit gate/up at M=16 must not be forced to one split.
+    DFLASH_VERIFY_QMM_KPARTS, when the user sets it, becomes the split count."""
+    assert verify_qmm.verify_route(16, 4096, 12288, 8) == ("mma2big", None)
+    assert verify_qmm.verify_route(16, 4096, 4096, 8) == ("mma2big_pipe", None)
+    assert verify_qmm.verify_route(16, 4128, 8224, 4) == ("mma2big", None)
+    monkeypatch.setenv("DFLASH_VERIFY_QMM_KPARTS", "4")
+    name, t = verify_qmm.verify_route(16, 4096, 12288, 8)
+    assert name == "mma2big" and (t.k_splits, t.waves_per_block) == (4, 4)
+    monkeypatch.setenv("DFLASH_VERIFY_QMM_KPARTS", "0")
+    assert verify_qmm.verify_route(16, 4096, 12288, 8) == ("mma2big", None)
+
+
+def test_module_dispatch_launch_shape(monkeypatch):
+    """VerifyQuantizedLinear's precomputed M=16 route uses the same launch
+    shape as verify_matmul (automatic unless DFLASH_VERIFY_QMM_KPARTS is set)."""
+    def forced(mod):  # launch-shape overrides captured by the module's call
+        return [c.cell_contents.k_splits for c in (mod._call_fn.__closure__ or ())
+                if hasattr(c.cell_contents, "k_splits")]
+
+    monkeypatch.setenv("DFLASH_VERIFY_QMM", "1")
+    assert forced(verify_linear.VerifyQuantizedLinear.from_quantized(_ql(4096, 12288, bits=8))) == []
+    monkeypatch.setenv("DFLASH_VERIFY_QMM_KPARTS", "4")
+    assert forced(verify_linear.VerifyQuantizedLinear.from_quantized(_ql(4096, 12288, bits=8))) == [4]
+
+
 @pytest.mark.parametrize("K,N,bits,gs,eligible", GOLD["eligibility"])
 def test_eligibility_known_answers(K, N, bits, gs, eligible):
     if K * bits % 32:

@@ -332,3 +332,139 @@ def test_gdn_reference_test_inputs():
         rep16 = oracle.to_f32(oracle.tape_replay(tape, k, g, state, k_dtype="f32",
                                                  state_dtype="bf16"), "bf16")
         assert np.all(np.abs(rep16 - s_out) <= 2 * 2.0 ** -8 * np.abs(s_out) + 1e-6)
+
+
+# ---------------------------------------------------------------- MoE routing / SwiGLU / combine
+#
+# Each check below is independent of the oracle's own formulas: brute force
+# with sorted(), math.exp and a bit-level bf16 rounding written here.
+
+def _bf16_round(v: float) -> float:
+    """float -> nearest bf16 value (via float32, round half to even on bits)."""
+    import struct
+
+    u = struct.unpack("<I", struct.pack("<f", v))[0]
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return struct.unpack("<f", struct.pack("<I", u))[0]
+
+
+def test_route_topk_brute_force_ties_and_renormalisation():
+    import math
+
+    rng = np.random.default_rng(31)
+    for trial in range(50):
+        E = int(rng.integers(2, 9))
+        k = int(rng.integers(1, E + 1))
+        lg = rng.integers(-3, 4, size=(3, E)).astype(np.float64) * 0.5  # many exact ties
+        ids, sc = oracle.route_topk(lg, k, renormalize=True)
+        ids_raw, sc_raw = oracle.route_topk(lg, k, renormalize=False)
+        assert np.array_equal(ids, ids_raw)
+        for t in range(3):
+            den = sum(math.exp(v) for v in lg[t])
+            p = [math.exp(v) / den for v in lg[t]]
+            # descending probability, lowest expert id first among equals
+            want = sorted(range(E), key=lambda e: (-p[e], e))[:k]
+            assert ids[t].tolist() == want
+            np.testing.assert_allclose(sc_raw[t], [p[e] for e in want], rtol=1e-6)
+            assert abs(float(sc[t].astype(np.float64).sum()) - 1.0) < 1e-6
+            np.testing.assert_allclose(sc[t], np.array([p[e] for e in want]) / sum(p[e] for e in want),
+                                       rtol=1e-6)
+
+
+def _expert_triple(E, N, K, rng, zero_expert=None):
+    ws = []
+    for e in range(E):
+        w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+        if e == zero_expert:
+            w[:] = 0.0
+        ws.append(oracle.quantize(w, 64, 4, out_dtype="bf16"))
+    return tuple(np.stack([w[i] for w in ws]) for i in range(3))
+
+
+def _deq_loop(trip, e, n, k):
+    """Dequantised weight by hand: nibble k%8 of word k//8, affine per group."""
+    wq, s, b = trip
+    q = (int(wq[e, n, k // 8]) >> (4 * (k % 8))) & 0xF
+    sc = float(oracle.bf16_bits_to_f32(s[e, n, k // 64]))
+    bi = float(oracle.bf16_bits_to_f32(b[e, n, k // 64]))
+    return q * sc + bi
+
+
+def test_switch_glu_zero_gate_gives_zero_h():
+    # an expert whose gate weights dequantise to 0 (scale = 1e-7 floor, codes
+    # and bias 0 for an all-zero group) has silu(0) = 0, so h = 0 whatever up is
+    rng = np.random.default_rng(32)
+    T, k, E, D, I = 2, 2, 3, 128, 64
+    gate = _expert_triple(E, I, D, rng, zero_expert=1)
+    up = _expert_triple(E, I, D, rng)
+    down = _expert_triple(E, D, I, rng)
+    assert not oracle.dequantize(gate[0][1], gate[1][1], gate[2][1], 64, 4, "f32").any()
+    x = oracle.f32_to_bf16_bits(rng.standard_normal((T, D)).astype(np.float32))
+    inds = np.array([[1, 0], [2, 1]])
+    h, y = oracle.switch_glu(x, inds, gate, up, down, group_size=64, dtype="bf16")
+    hf = oracle.bf16_bits_to_f32(h)
+    assert not hf[0].any() and not hf[3].any()       # pairs on expert 1
+    assert hf[1].any() and hf[2].any()
+    # the down projection of a zero activation row is exactly zero
+    yf = oracle.bf16_bits_to_f32(y)
+    assert not yf[0].any() and not yf[3].any()
+    assert yf[1].any() and yf[2].any()
+
+
+def test_switch_glu_element_loop():
+    """2 tokens x 64 -> 64 (k = 2 of 3 experts) against an element-by-element
+    loop with math.exp and bf16 rounding after gate, up, sigmoid, gate * sig
+    and * up (MLX rounds every op to the activation dtype)."""
+    import math
+
+    rng = np.random.default_rng(33)
+    T, k, E, D, I = 2, 2, 3, 64, 64
+    gate, up, down = (_expert_triple(E, I, D, rng), _expert_triple(E, I, D, rng),
+                      _expert_triple(E, D, I, rng))
+    x = oracle.f32_to_bf16_bits(rng.standard_normal((T, D)).astype(np.float32))
+    xf = oracle.bf16_bits_to_f32(x).astype(np.float64)
+    inds = np.array([[2, 0], [1, 2]])
+    h, y = oracle.switch_glu(x, inds, gate, up, down, group_size=64, dtype="bf16")
+    for t in range(T):
+        for j in range(k):
+            e = int(inds[t, j])
+            hrow = []
+            for n in range(I):
+                g = _bf16_round(sum(xf[t, kk] * _deq_loop(gate, e, n, kk) for kk in range(D)))
+                u = _bf16_round(sum(xf[t, kk] * _deq_loop(up, e, n, kk) for kk in range(D)))
+                sig = _bf16_round(1.0 / (1.0 + math.exp(-g)))
+                hv = _bf16_round(_bf16_round(g * sig) * u)
+                hrow.append(hv)
+            got_h = oracle.bf16_bits_to_f32(h[t * k + j]).astype(np.float64)
+            # bit-exact: both sides round every op's float64 value to bf16
+            # (a dropped rounding point changes some of the 512 values)
+            assert got_h.tolist() == hrow
+            for n in range(0, D, 7):
+                want = _bf16_round(sum(hrow[i] * _deq_loop(down, e, n, i) for i in range(I)))
+                assert float(oracle.bf16_bits_to_f32(y[t * k + j, n])) == want
+
+
+def test_moe_combine_one_hot_and_slot_permutation():
+    rng = np.random.default_rng(34)
+    T, k, D = 4, 3, 40
+    y = oracle.f32_to_bf16_bits(rng.standard_normal((T * k, D)).astype(np.float32))
+    # one-hot scores pick the selected pair's row exactly
+    sel = rng.integers(0, k, size=T)
+    sc = np.zeros((T, k), np.float32)
+    sc[np.arange(T), sel] = 1.0
+    out = oracle.moe_combine(y, sc, dtype="bf16", out_dtype="bf16")
+    for t in range(T):
+        assert np.array_equal(out[t], y[t * k + sel[t]])
+    # permuting the k slots of each token (rows and scores together) leaves
+    # the sum unchanged
+    sc = rng.random((T, k)).astype(np.float32)
+    base = oracle.moe_combine(y, sc, dtype="bf16")
+    perm = np.stack([rng.permutation(k) for _ in range(T)])
+    y_p = y.reshape(T, k, D)[np.arange(T)[:, None], perm].reshape(T * k, D)
+    sc_p = sc[np.arange(T)[:, None], perm]
+    np.testing.assert_allclose(oracle.moe_combine(y_p, sc_p, dtype="bf16"), base, rtol=1e-12)
+    # and equals a plain loop
+    yf = oracle.bf16_bits_to_f32(y).astype(np.float64)
+    for t in range(T):
+        want = sum(float(sc[t, j]) * yf[t * k + j] for j in range(k))
+        np.testing.assert_allclose(base[t], want, rtol=1e-12)

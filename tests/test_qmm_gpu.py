@@ -65,10 +65,12 @@ def test_baseline_layer_shapes_m16(dev, K, N):
 
 
 @pytest.mark.parametrize("M", [4, 8, 32])
-@pytest.mark.parametrize("K,N", [(4096, 12288), (4096, 1024), (17408, 5120), (5120, 17408)])
+@pytest.mark.parametrize("K,N", [(4096, 12288), (4096, 1024), (17408, 5120), (5120, 17408),
+                                 (5120, 5120), (5120, 1024)])
 def test_layer_shapes_other_m(dev, M, K, N):
-    """The adaptive M=4 block and the 27B sweep's M=8 / M=32 on the layer
-    shapes they run at."""
+    """The adaptive M=4 block and the 27B sweep's M=8 / M=32 on every layer
+    shape they run at (q/o 5120x5120 and k/v 5120x1024 take their own split
+    plans, e.g. 3 splits at M=32 on 5120x5120)."""
     x, w_q, s, b = make_qmm_case(M, K, N, 64, seed=K + N + M)
     _check(_run(dev, x, w_q, s, b, 64), x, w_q, s, b, 64)
 
@@ -128,15 +130,13 @@ def test_closed_form_exact(dev):
     x = oracle.f32_to_bf16_bits(xf)
     want = oracle.quantized_matmul(x, w_q, s, b, group_size=gs, out_dtype="bf16")
     for tuning in (None, (1, 1, 1, 0), (1, 2, 4, 0), (1, 4, 8, 0), (1, 1, 3, 0), (2, 1, 0, 1),
-                   (2, 2, 0, 1), (2, 1, 0, 3), (2, 2, 0, 2), (3, 1, 1, 0), (3, 2, 4, 0),
-                   (3, 4, 3, 0), (3, 1, 8, 0)):
+                   (2, 2, 0, 1), (2, 1, 0, 3), (2, 2, 0, 2), (2, 0, 8, 2), (2, 0, 4, 4)):
         got = _run(dev, x, w_q, s, b, gs, tuning=_tuning(tuning))
         assert np.array_equal(got, want), f"tuning {tuning}"
 
 
 def _tuning(t):
-    """(path, tiles_per_wave, waves_per_block, k_splits); path 1 general, 2 streaming,
-    3 register-direct."""
+    """(path, tiles_per_wave, waves_per_block, k_splits); path 1 general, 2 streaming."""
     if t is None:
         return None
     from dflash_mlx_amd import _lib
@@ -162,32 +162,6 @@ def test_streaming_kernel_shapes(dev, M, gs):
     x, w_q, s, b = make_qmm_case(M, K, N, gs, seed=M * 3 + gs)
     for t in ((2, 0, 0, 1), (2, 0, 0, 3), (2, 2, 0, 2)):
         _check(_run(dev, x, w_q, s, b, gs, tuning=_tuning(t)), x, w_q, s, b, gs)
-
-
-@pytest.mark.parametrize("M", [1, 4, 8, 13, 16])
-@pytest.mark.parametrize("gs", [32, 64, 128])
-def test_direct_kernel_shapes(dev, M, gs):
-    # forced onto the register-direct kernel: every tile count, K split and a
-    # ragged N (the last workgroup's rows past N are clamped loads, never stored)
-    K, N = 2048, 632
-    x, w_q, s, b = make_qmm_case(M, K, N, gs, seed=M * 5 + gs)
-    for t in ((3, 1, 1, 0), (3, 2, 3, 0), (3, 4, 8, 0), (3, 1, 5, 0)):
-        _check(_run(dev, x, w_q, s, b, gs, tuning=_tuning(t)), x, w_q, s, b, gs)
-
-
-@pytest.mark.parametrize("gs", [32, 64, 128])
-def test_direct_kernel_f16(dev, gs):
-    M, K, N = 16, 1536, 520
-    x, w_q, s, b = make_qmm_case(M, K, N, gs, dtype="f16", seed=gs + 1)
-    for t in ((3, 1, 2, 0), (3, 2, 6, 0)):
-        _check(_run(dev, x, w_q, s, b, gs, "f16", tuning=_tuning(t)), x, w_q, s, b, gs, "f16")
-
-
-@pytest.mark.parametrize("K,N", [(4096, 4096), (4096, 1024), (4096, 12288), (12288, 4096),
-                                 (5120, 17408), (17408, 5120)])
-def test_direct_kernel_layer_shapes(dev, K, N):
-    x, w_q, s, b = make_qmm_case(16, K, N, 64, seed=K + N)
-    _check(_run(dev, x, w_q, s, b, 64, tuning=_tuning((3, 0, 0, 0))), x, w_q, s, b, 64)
 
 
 def test_deterministic_and_workspace_reuse(dev):
@@ -219,10 +193,12 @@ def test_unsupported_raises(dev):
 
 @pytest.mark.parametrize("M,K,N,gs", [
     (16, 4096, 1024, 64),   # streaming, 8 wavefronts, K split 4 ways
-    (4, 512, 96, 32),       # streaming, 8 wavefronts, one step, ragged N
-    (16, 1024, 2048, 128),  # streaming, 8 wavefronts
+    (4, 512, 96, 32),       # streaming, 4 wavefronts in two LDS stages, one step, ragged N
+    (16, 1024, 2048, 128),  # streaming, 4 wavefronts in two LDS stages
     (24, 2048, 200, 64),    # streaming, 4 wavefronts, two 16-row activation blocks
     (16, 512, 16448, 64),   # streaming, 4 wavefronts (257 blocks), unsplit
+    (16, 4096, 12288, 64),  # streaming, 4 wavefronts in two stages, K split 2 ways (the 9B gate/up plan)
+    (16, 2048, 12288, 64),  # the same plan at 4 steps per split
     (33, 256, 40, 64),      # register-load kernel (M > 32)
     (1, 96, 16, 32)])       # register-load kernel (K not whole 256-k steps)
 @pytest.mark.parametrize("dtype", ["bf16", "f16"])

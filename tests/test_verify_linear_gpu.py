@@ -1,0 +1,173 @@
+"""The drop-in module on the GPU: the reference's bit-identity invariants for
+``VerifyQuantizedLinear`` (tests/test_verify_linear_parity.py:41-138) and the
+disabled-path identity of ``verify_matmul``
+(tests/test_verify_qmm_parity.py:102-106), restated with this framework's
+modules; plus the bias add (dflash_mlx/verify_linear.py:250,261) and 8-bit
+modules on the 9B layer shapes against the oracle.
+
+Bit-identity is the reference's own bar for these (``allclose(atol=0,
+rtol=0)``); tolerance checks use the oracle and the 1e-2 metric."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from tests.conftest import from_dev
+
+pytestmark = pytest.mark.gpu
+
+REL_TOL = 1e-2
+
+
+def _mk_ql(dev, K, N, *, bits=4, gs=64, bias=False, seed=0, std=0.1):
+    import torch
+
+    from dflash_mlx_amd.verify_linear import QuantizedLinear
+
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    lin = torch.nn.Linear(K, N, bias=bias)
+    with torch.no_grad():
+        lin.weight.copy_((torch.randn((N, K), generator=g) * std).to(torch.bfloat16))
+        if bias:
+            lin.bias.copy_(torch.randn((N,), generator=g))
+    ql = QuantizedLinear.from_linear(lin.to(dev), group_size=gs, bits=bits, dtype=torch.bfloat16)
+    return ql
+
+
+def _x(dev, M, K, seed=1, scale=0.5):
+    import torch
+
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    return (torch.randn((M, K), generator=g) * scale).to(torch.bfloat16).to(dev)
+
+
+def _direct(ql, x):
+    from dflash_mlx_amd.verify_qmm import verify_matmul
+
+    return verify_matmul(x, ql.weight, ql.scales, ql.biases, transpose=True,
+                         group_size=ql.group_size, bits=ql.bits)
+
+
+def _oracle_check(ql, x, y):
+    import torch
+
+    xs = from_dev(x, "bf16")
+    w = ql.weight.cpu().numpy().view(np.uint32)
+    s = from_dev(ql.scales, "bf16")
+    b = from_dev(ql.biases, "bf16")
+    want = oracle.quantized_matmul(xs, w, s, b, group_size=ql.group_size, bits=ql.bits)
+    if ql.has_bias():
+        want = want + oracle.to_f32(from_dev(ql.bias, "bf16"), "bf16")
+    got = oracle.to_f32(from_dev(y, "bf16"), "bf16")
+    _, rel = oracle.parity_metrics(got, want)
+    assert rel <= REL_TOL, rel
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("M", [1, 8, 32])
+def test_parity_non_verify_is_stock(dev, monkeypatch, M):
+    # test_verify_linear_parity.py:41-49: M outside {4, 16} routes through
+    # the stock matmul, bit-identical to the unswapped module
+    import torch
+
+    from dflash_mlx_amd.verify_linear import VerifyQuantizedLinear
+
+    monkeypatch.setenv("DFLASH_VERIFY_QMM", "1")
+    ql = _mk_ql(dev, 512, 1024)
+    verify = VerifyQuantizedLinear.from_quantized(ql)
+    x = _x(dev, M, 512)
+    assert torch.equal(verify(x), ql(x))
+
+
+@pytest.mark.parametrize("M,K,N", [(16, 512, 1024), (16, 512, 16), (4, 512, 1024), (4, 64, 12),
+                                   (16, 4096, 12288), (4, 5120, 1024)])
+def test_wrapper_matches_direct_bitwise(dev, monkeypatch, M, K, N):
+    # test_verify_linear_parity.py:51-72 (M=16, N=1024 and N=16) and 116-138
+    # (M=4, N=1024 and N=12), plus two layer shapes
+    import torch
+
+    from dflash_mlx_amd.verify_linear import VerifyQuantizedLinear, is_verify_eligible
+
+    monkeypatch.setenv("DFLASH_VERIFY_QMM", "1")
+    ql = _mk_ql(dev, K, N, seed=K + N)
+    assert is_verify_eligible(ql)
+    verify = VerifyQuantizedLinear.from_quantized(ql)
+    x = _x(dev, M, K, seed=M)
+    y_verify = verify(x)
+    assert torch.equal(y_verify, _direct(ql, x))
+    _oracle_check(ql, x, y_verify)
+
+
+@pytest.mark.parametrize("variant", ["combo_ktmpl", "super_tree_fp16_ktmpl"])
+def test_wrapper_honors_forced_variant(dev, monkeypatch, variant):
+    # test_verify_linear_parity.py:74-114: a forced variant, wrapper == direct
+    # bitwise and both within the reference's bounds of the stock result
+    import torch
+
+    from dflash_mlx_amd.verify_linear import VerifyQuantizedLinear
+
+    monkeypatch.setenv("DFLASH_VERIFY_QMM", "1")
+    monkeypatch.setenv("DFLASH_VERIFY_VARIANT", variant)
+    ql = _mk_ql(dev, 512, 1024, seed=3)
+    verify = VerifyQuantizedLinear.from_quantized(ql)
+    x = _x(dev, 16, 512, seed=4)
+    y_direct, y_verify = _direct(ql, x), verify(x)
+    assert torch.equal(y_direct, y_verify)
+    y_stock = ql(x).float()
+    ref_max = float(y_stock.abs().max())
+    for y in (y_direct.float(), y_verify.float()):
+        d = float((y - y_stock).abs().max())
+        assert d <= 6e-2 and d / (ref_max + 1e-3) <= 5e-2
+
+
+@pytest.mark.parametrize("K,N", [(5120, 8), (512, 1024)])
+def test_disabled_path_is_exactly_stock(dev, K, N):
+    # test_verify_qmm_parity.py:102-106: DFLASH_VERIFY_QMM unset -> the stock result
+    import torch
+
+    from dflash_mlx_amd.verify_qmm import is_enabled, quantized_matmul
+
+    assert not is_enabled()
+    ql = _mk_ql(dev, K, N, seed=5)
+    x = _x(dev, 16, K, seed=6)
+    y_stock = quantized_matmul(x, ql.weight, ql.scales, ql.biases, group_size=64, bits=4)
+    assert torch.equal(_direct(ql, x), y_stock)
+
+
+@pytest.mark.parametrize("M", [16, 4, 8])
+def test_bias_add(dev, monkeypatch, M):
+    # verify_linear.py:250,261: y = verify_matmul(x) + bias on every route
+    import torch
+
+    from dflash_mlx_amd.verify_linear import VerifyQuantizedLinear
+
+    monkeypatch.setenv("DFLASH_VERIFY_QMM", "1")
+    ql = _mk_ql(dev, 1024, 512, bias=True, seed=7)
+    assert ql.has_bias()
+    verify = VerifyQuantizedLinear.from_quantized(ql)
+    x = _x(dev, M, 1024, seed=8)
+    y = verify(x)
+    assert torch.equal(y, _direct(ql, x) + ql.bias)
+    assert torch.equal(y, ql(x))
+    _oracle_check(ql, x, y)
+
+
+@pytest.mark.parametrize("K,N", [(4096, 4096), (4096, 1024), (4096, 12288), (12288, 4096)])
+def test_8bit_module_on_layer_shapes(dev, monkeypatch, K, N):
+    """8-bit modules at M=16 with the verify kernels on (mma2big routes): the
+    automatic plan, wrapper == direct bitwise, and within 1e-2 of the oracle."""
+    import torch
+
+    from dflash_mlx_amd.verify_linear import VerifyQuantizedLinear
+    from dflash_mlx_amd.verify_qmm import verify_route
+
+    monkeypatch.setenv("DFLASH_VERIFY_QMM", "1")
+    assert verify_route(16, K, N, 8)[1] is None
+    ql = _mk_ql(dev, K, N, bits=8, seed=K + N, std=0.02)
+    verify = VerifyQuantizedLinear.from_quantized(ql)
+    x = _x(dev, 16, K, seed=9, scale=1.0)
+    y = verify(x)
+    assert torch.equal(y, _direct(ql, x))
+    _oracle_check(ql, x, y)
