@@ -1,32 +1,34 @@
 #!/usr/bin/env python3
 """Benchmark of the verify-path int4 matmuls on one MI355X.
 
-Default workload: the 9B-class dense verify-linear sweep -- 32 layers x
-{q 4096->4096, k 4096->1024, v 4096->1024, o 4096->4096, gate 4096->12288,
-up 4096->12288, down 12288->4096}, int4 affine group_size 64, bf16 x [16, K]
-~ N(0,1) per call, W ~ N(0, 0.02) quantised on the GPU before timing.  One
-step = the 224 verify matmuls of one verify pass, replayed from a HIP graph
-(``--no-graph``: eager launches).  All weights (3.55 GB) are resident in HBM
-and the pass streams every byte once, so the 256 MB infinity cache cannot
-hold the working set.
+Default line: the 27B-class dense verify-linear sweep at M = 16 -- 64 layers
+x {q 5120->5120, k 5120->1024, v 5120->1024, o 5120->5120, gate
+5120->17408, up 5120->17408, down 17408->5120}, int4 affine group_size 64,
+bf16 activations ~ N(0,1), W ~ N(0, 0.02) quantised on the GPU before
+timing.  One step = the 448 verify matmuls of one verify pass, replayed from
+a HIP graph (``--no-graph``: eager launches).  All weights (12.1 GB) are
+resident in HBM and the pass streams every byte once, so the 256 MB
+infinity cache cannot hold the working set.
 
-Prints one JSON line: value = algorithmic GB/s of the step (packed weights +
-bf16 scales/biases + x + y), us_per_call, the HBM roofline of the dominant
-kernel (its launches replayed alone and timed with HIP events on the stream
-they run on; ``traffic`` = measured HBM bytes per launch from the rocprofv3
+The JSON line: value = algorithmic GB/s of the step (packed weights + bf16
+scales/biases + x + y), us_per_call, the HBM roofline of the dominant kernel
+(its launches replayed alone and timed with HIP events on the stream they
+run on; ``traffic`` = measured HBM bytes per launch from the rocprofv3
 FETCH_SIZE / WRITE_SIZE summary in profiles/, when one exists for this
 workload and kernel; ``mfma`` = its algorithmic TFLOP/s against the dense
 bf16 peak and the MFMA-busy share from the rocprofv3 counter summary) and a
 CPU baseline (the oracle's C restatement on this host's cores, on a bounded
 sample: layer 0's seven matmuls).
 
-Other workloads (``--workload``, not the default line): ``27b`` (64 layers,
-hidden 5120, ``--m`` 8/16/32), ``single`` ([16,4096]x[4096,4096], weights
-rotated over a 1 GB pool), ``lmhead`` (fused lm_head [16,5120]x[151936,5120]
-+ greedy accept), ``moe`` (40 layers of top-8-of-256 routed experts,
-hidden 2048, expert width 512) and ``gdn`` (the GDN rollback pair of a verify
-cycle: gated delta + tape over 16 steps, replay of 9, per layer).  ``copy``
-is a 512 MiB device copy used to calibrate the HBM traffic counters.
+``configs`` holds the other benchmarked workloads, each with the same
+fields: ``single`` ([16,4096]x[4096,4096], weights rotated over a 1 GB
+pool), ``9b`` (the 9B-class sweep: 32 layers, hidden 4096), ``27b_m8`` /
+``27b_m32`` (the 27B sweep at M = 8 / 32), ``moe`` (40 layers of top-8-of-256
+routed experts, hidden 2048, expert width 512) and ``lmhead`` (fused lm_head
+[16,5120]x[151936,5120] + greedy accept).  ``--workload X`` prints only X's
+line (for profiling runs); ``gdn`` (the GDN rollback pair) and ``copy`` (a
+512 MiB device copy that calibrates the traffic counters) exist only that
+way.
 """
 
 from __future__ import annotations
@@ -47,6 +49,8 @@ METRIC = "M=16 int4 verify_qmm µs/call + achieved HBM GB/s (% of peak), 1 GPU"
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 MFMA_FILE = os.path.join(ROOT, "profiles", "mfma.json")
 MFMA_PEAK_TFLOPS = 2500.0  # dense bf16 MFMA, MI355X
+CPU_LABEL = "own CPU restatement, not MLX (oracle/cpu_qmm.c, OpenMP, fp32 accumulate)"
+CPU_SAMPLE_S = 4.0  # seconds of CPU work per configuration's baseline
 
 SHAPES_9B = [("q", 4096, 4096), ("k", 4096, 1024), ("v", 4096, 1024), ("o", 4096, 4096),
              ("gate", 4096, 12288), ("up", 4096, 12288), ("down", 12288, 4096)]
@@ -99,50 +103,84 @@ def time_replays(torch, g, reps, warmup=2):
     return e0.elapsed_time(e1) / reps
 
 
-def cpu_baseline(torch, layer, M):
-    """Oracle C restatement (fp32 accumulate, OpenMP) on this host, layer 0's
-    seven matmuls; GB/s of algorithmic bytes."""
+# ---------------------------------------------------------------- CPU baseline
+
+def cpu_threads():
+    n = len(os.sched_getaffinity(0))
+    try:
+        n = min(n, int(os.environ.get("OMP_NUM_THREADS", n)))
+    except ValueError:
+        pass
+    return max(1, n)
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown CPU"
+
+
+def _host16(torch, t):
     import numpy as np
 
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def _host_words(t):
+    import numpy as np
+
+    return t.contiguous().cpu().numpy().view(np.uint32)
+
+
+def _cpu_loop(work, nbytes, what):
+    """Run work() (one sample unit of nbytes algorithmic bytes) for about
+    CPU_SAMPLE_S seconds after one warm-up; GB/s on this host."""
+    work()
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        work()
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= CPU_SAMPLE_S or reps >= 1000:
+            break
+    gbs = nbytes * reps / el / 1e9
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": cpu_threads(), "kind": "port",
+            "label": CPU_LABEL,
+            "sample": f"{what} x {reps} reps, {el:.1f} s on {cpu_model()}"}
+
+
+def cpu_loaded():
     from oracle import cpu as ocpu
 
     try:
         ocpu.load()
+        return ocpu
     except OSError as exc:  # not built on this host
         log(f"cpu baseline skipped: {exc}")
         return None
-    threads = len(os.sched_getaffinity(0))
-    host = []
-    total = 0
-    for (x, w_q, s, b, y) in layer:
-        hx = x.view(torch.int16).cpu().numpy().view(np.uint16)
-        hw = w_q.cpu().numpy().view(np.uint32)
-        hs = s.view(torch.int16).cpu().numpy().view(np.uint16)
-        hb = b.view(torch.int16).cpu().numpy().view(np.uint16)
-        host.append((hx, hw, hs, hb))
-        total += alg_bytes(M, hx.shape[1], hw.shape[0])
-    ocpu.qmm_bf16(*host[0], 64, 4, threads)  # warm
-    reps, t0 = 0, time.perf_counter()
-    while True:
+
+
+def cpu_baseline_calls(torch, calls, M, what):
+    """The oracle C restatement over a list of (x, w_q, s, b, ...) matmuls."""
+    ocpu = cpu_loaded()
+    if ocpu is None:
+        return None
+    threads = cpu_threads()
+    host = [(_host16(torch, c[0]), _host_words(c[1]), _host16(torch, c[2]), _host16(torch, c[3]))
+            for c in calls]
+    total = sum(alg_bytes(M, h[0].shape[1], h[1].shape[0]) for h in host)
+
+    def work():
         for args in host:
             ocpu.qmm_bf16(*args, 64, 4, threads)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= 10.0 or reps >= 400:  # a bounded sample of about 10 s of CPU work
-            break
-    gbs = total * reps / el / 1e9
-    cpu_model = ""
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu_model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
-    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"layer 0 of the sweep ({len(host)} matmuls, M={M}) x {reps} reps, "
-                      f"{el:.1f} s, oracle/cpu_qmm.c OpenMP fp32-accumulate on {cpu_model}"}
+    return _cpu_loop(work, total, what)
 
+
+# ---------------------------------------------------------------- reports
 
 def measured_traffic(workload, kernel):
     """HBM bytes per launch from the committed rocprofv3 PMC summary, or None."""
@@ -172,73 +210,119 @@ def mfma_report(workload, kernel, flops, us):
             "busy_pct_counter": util}
 
 
-def base_result(args, value, ms, n_calls, config, roofline):
-    return {
-        "metric": METRIC,
-        "value": round(value, 2),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms, 4),
-        "us_per_call": round(ms * 1e3 / n_calls, 3),
-        "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights quantised int4 gs64 on GPU)",
-        "config": config,
-        "roofline": roofline,
-    }
+def roofline_of(workload, kernel, nbytes, us, flops, per_kernel=None):
+    gbs = nbytes / (us * 1e-6) / 1e9
+    r = {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(workload, kernel),
+         "kernel": kernel, "bytes_per_launch": int(nbytes), "us_per_launch": round(us, 3)}
+    if per_kernel is not None:
+        r["per_kernel"] = per_kernel
+    r["mfma"] = mfma_report(workload, kernel, flops, us)
+    return r
 
 
-def run_sweep(args, torch):
+def line(value_gbs, ms, n_calls, config, roofline, cpu=None):
+    out = {"value": round(value_gbs, 2), "unit": "GB/s", "ms_per_step": round(ms, 4),
+           "us_per_call": round(ms * 1e3 / n_calls, 3),
+           "pct_of_hbm_peak": round(100 * value_gbs / HBM_PEAK_GBS, 2),
+           "config": config, "roofline": roofline}
+    if cpu is not None:
+        out["cpu_baseline"] = cpu
+    return out
+
+
+# ---------------------------------------------------------------- workloads
+
+class Sweep:
+    """Weights of a dense sweep (built once; reused at every M)."""
+
+    def __init__(self, torch, big, bits):
+        from dflash_mlx_amd.quantize import quantize
+
+        self.torch = torch
+        self.dev = torch.device("cuda:0")
+        self.big = big
+        self.bits = bits
+        self.shapes = SHAPES_27B if big else SHAPES_9B
+        self.layers = 64 if big else 32
+        gen = torch.Generator(device=self.dev)
+        t0 = time.time()
+        self.weights = []
+        for l in range(self.layers):
+            gen.manual_seed(100 + l)
+            for (_, K, N) in self.shapes:
+                self.weights.append(make_weights(torch, quantize, K, N, gen, self.dev, bits=bits))
+        torch.cuda.synchronize()
+        log(f"{'27b' if big else '9b'} weights ready: {len(self.weights)} matrices, "
+            f"{time.time() - t0:.1f} s")
+
+    def launches(self, M, fuse):
+        """The step's launches: ``(x, [(w, s, b)], [y])``.  Unfused, every
+        matmul reads its own activations; fused, q/k/v share one input and
+        gate/up another (as in the model), one launch each."""
+        torch = self.torch
+        groups = [[0, 1, 2], [3], [4, 5], [6]] if fuse else [[i] for i in range(7)]
+        out = []
+        for l in range(self.layers):
+            for grp in groups:
+                i0 = l * len(self.shapes) + grp[0]
+                mats = [self.weights[l * len(self.shapes) + i] for i in grp]
+                K = mats[0][0].shape[1] * 32 // self.bits
+                xg = torch.Generator(device=self.dev)
+                xg.manual_seed(10000 + i0)
+                x = torch.randn((M, K), generator=xg, device=self.dev).to(torch.bfloat16)
+                ys = [torch.empty((M, w.shape[0]), dtype=torch.bfloat16, device=self.dev)
+                      for (w, _, _) in mats]
+                out.append((x, mats, ys))
+        return out
+
+
+def launch_bytes(M, x, mats, bits):
+    """Algorithmic bytes of one launch: every matrix's packed weights, scales
+    and biases and output rows, the shared activations once."""
+    K = x.shape[1]
+    return 2 * M * K + sum(alg_bytes(M, K, w.shape[0], bits=bits) - 2 * M * K
+                           for (w, _, _) in mats)
+
+
+def run_sweep(args, torch, sweep, M, name, with_cpu=True, fuse=True):
     from dflash_mlx_amd import _lib, _runtime
-    from dflash_mlx_amd.quantize import quantize
-    from dflash_mlx_amd.verify_qmm import qmm_launch
+    from dflash_mlx_amd.verify_qmm import qmm_launch, qmm_multi_launch
 
-    dev = torch.device("cuda:0")
-    big = args.workload == "27b"
-    shapes = SHAPES_27B if big else SHAPES_9B
-    layers = 64 if big else 32
-    M, bits = args.m, args.bits
-    gen = torch.Generator(device=dev)
-    calls = []
-    t0 = time.time()
-    for l in range(layers):
-        gen.manual_seed(100 + l)
-        for j, (_, K, N) in enumerate(shapes):
-            w_q, s, b = make_weights(torch, quantize, K, N, gen, dev, bits=bits)
-            xg = torch.Generator(device=dev)
-            xg.manual_seed(10000 + l * len(shapes) + j)
-            x = torch.randn((M, K), generator=xg, device=dev).to(torch.bfloat16)
-            y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
-            calls.append((x, w_q, s, b, y))
-    torch.cuda.synchronize()
-    log(f"weights ready: {len(calls)} matmuls, {time.time() - t0:.1f} s")
-    step_bytes = sum(alg_bytes(M, x.shape[1], w.shape[0], bits=bits)
-                     for (x, w, _, _, _) in calls)
-
+    bits = sweep.bits
+    fuse = fuse and not (args.path or args.tiles or args.splits)
+    calls = sweep.launches(M, fuse)
+    step_bytes = sum(launch_bytes(M, x, mats, bits) for (x, mats, _) in calls)
     tuning = None
     if args.path or args.tiles or args.splits:
         tuning = _lib.QmmTuning(args.path, args.tiles, args.splits, args.splits)
     lib = _lib.load()
     tptr = ctypes.byref(tuning) if tuning is not None else None
-    need = max(lib.dfmi_qmm_workspace_bytes_ex(M, x.shape[1], w.shape[0], 64, bits, tptr)
-               for (x, w, _, _, _) in calls)
+    need = 0
+    for (x, mats, _) in calls:
+        K = x.shape[1]
+        if len(mats) == 1:
+            need = max(need, lib.dfmi_qmm_workspace_bytes_ex(M, K, mats[0][0].shape[0], 64, bits,
+                                                             tptr))
+        else:
+            ns = (ctypes.c_int64 * len(mats))(*[w.shape[0] for (w, _, _) in mats])
+            need = max(need, lib.dfmi_qmm_multi_workspace_bytes(M, K, ns, len(mats), 64, bits))
 
     def launches(subset):
         def fn():
-            for (x, w_q, s, b, y) in subset:
-                qmm_launch(x, w_q, s, b, w_q.shape[0], 64, bits, tuning, out=y)
+            for (x, mats, ys) in subset:
+                if len(mats) == 1:
+                    w_q, s, b = mats[0]
+                    qmm_launch(x, w_q, s, b, w_q.shape[0], 64, bits, tuning, out=ys[0])
+                else:
+                    qmm_multi_launch(x, mats, 64, bits, outs=ys)
         return fn
 
     if args.no_graph:
         stream = torch.cuda.Stream()
         step = launches(calls)
         with torch.cuda.stream(stream):
-            _runtime.WORKSPACES.reserve(dev, need)
+            _runtime.WORKSPACES.reserve(sweep.dev, need)
             for _ in range(args.warmup):
                 step()
         torch.cuda.synchronize()
@@ -253,60 +337,72 @@ def run_sweep(args, torch):
     else:
         g = graph_of(torch, launches(calls))
         ms = time_replays(torch, g, args.steps, warmup=args.warmup)
-    log(f"timed {args.steps} steps: {ms:.3f} ms/step")
+        del g
+    log(f"{name}: {ms:.3f} ms/step ({len(calls)} launches)")
     gbs = step_bytes / (ms * 1e-3) / 1e9
 
-    # dominant kernel: the calls of each kernel replayed alone
+    # each kernel's launches replayed alone
     groups = {}
     for c in calls:
-        name = lib.dfmi_qmm_kernel_name(M, c[0].shape[1], c[1].shape[0], 64, bits, tptr).decode()
-        groups.setdefault(name, []).append(c)
+        x, mats, _ = c
+        N0 = mats[0][0].shape[0]
+        kname = None
+        if len(mats) > 1:
+            ns = (ctypes.c_int64 * len(mats))(*[w.shape[0] for (w, _, _) in mats])
+            kname = lib.dfmi_qmm_multi_kernel_name(M, x.shape[1], ns, len(mats), 64, bits)
+        if kname is None:
+            kname = lib.dfmi_qmm_kernel_name(M, x.shape[1], N0, 64, bits, tptr)
+        groups.setdefault(kname.decode(), []).append(c)
     per_kernel = {}
     reps = max(3, args.steps // 4)
-    for name, subset in groups.items():
+    for kname, subset in groups.items():
         gk = graph_of(torch, launches(subset))
         kms = time_replays(torch, gk, reps)
         del gk
-        kbytes = sum(alg_bytes(M, x.shape[1], w.shape[0], bits=bits)
-                     for (x, w, _, _, _) in subset)
-        per_kernel[name] = {"launches_per_step": len(subset), "ms_per_step": round(kms, 4),
-                            "us_per_launch": round(kms * 1e3 / len(subset), 3),
-                            "bytes_per_launch": kbytes // len(subset),
-                            "flops_per_launch": sum(2 * M * x.shape[1] * w.shape[0]
-                                                    for (x, w, _, _, _) in subset) // len(subset),
-                            "GBps": round(kbytes / (kms * 1e-3) / 1e9, 2)}
+        kbytes = sum(launch_bytes(M, x, mats, bits) for (x, mats, _) in subset)
+        kflops = sum(2 * M * x.shape[1] * w.shape[0] for (x, mats, _) in subset
+                     for (w, _, _) in mats)
+        per_kernel[kname] = {"launches_per_step": len(subset), "ms_per_step": round(kms, 4),
+                             "us_per_launch": round(kms * 1e3 / len(subset), 3),
+                             "bytes_per_launch": kbytes // len(subset),
+                             "flops_per_launch": kflops // len(subset),
+                             "GBps": round(kbytes / (kms * 1e-3) / 1e9, 2)}
     dom = max(per_kernel, key=lambda k: per_kernel[k]["ms_per_step"])
     d = per_kernel[dom]
-    roofline = {"bound": "hbm", "achieved": d["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(d["GBps"] / HBM_PEAK_GBS, 4),
-                "traffic": measured_traffic(args.workload, dom),
-                "kernel": dom, "bytes_per_launch": d["bytes_per_launch"],
-                "us_per_launch": d["us_per_launch"], "per_kernel": per_kernel}
-    roofline["mfma"] = mfma_report(args.workload + ("_bits8" if bits == 8 else ""), dom,
-                                   d["flops_per_launch"], d["us_per_launch"])
-    config = {"workload": f"{args.workload}-class dense verify-linear sweep",
-              "layers": layers, "linears_per_layer": len(shapes), "M": M, "group_size": 64,
-              "bits": bits, "launch": "eager" if args.no_graph else "hip-graph",
-              "algorithmic_bytes_per_step": step_bytes}
-    res = base_result(args, gbs, ms, len(calls), config, roofline)
-    if not args.no_cpu and args.workload == "9b" and bits == 4:
-        res["cpu_baseline"] = cpu_baseline(torch, calls[:len(shapes)], M)
-    return res
+    wl = ("27b" if sweep.big else "9b") + ("" if M == 16 else f"_m{M}") + \
+        ("_bits8" if bits == 8 else "")
+    roofline = roofline_of(wl, dom, d["bytes_per_launch"], d["us_per_launch"],
+                           d["flops_per_launch"], per_kernel)
+    config = {"workload": f"{'27b' if sweep.big else '9b'}-class dense verify-linear sweep",
+              "layers": sweep.layers, "linears_per_layer": len(sweep.shapes), "M": M,
+              "group_size": 64, "bits": bits,
+              "launch": ("eager" if args.no_graph else "hip-graph") +
+                        (", q/k/v and gate/up each one shared-activation launch" if fuse
+                         else ", one launch per matmul"),
+              "launches_per_step": len(calls), "algorithmic_bytes_per_step": step_bytes}
+    cpu = None
+    if with_cpu and not args.no_cpu and bits == 4:
+        layer0 = [(x, w_q, s, b) for (x, mats, _) in calls[:len(calls) // sweep.layers]
+                  for (w_q, s, b) in mats]
+        cpu = cpu_baseline_calls(torch, layer0, M,
+                                 f"layer 0 of the sweep ({len(sweep.shapes)} matmuls, M={M})")
+    del calls
+    return line(gbs, ms, len(sweep.weights), config, roofline, cpu)
 
 
 def run_single(args, torch):
+    from dflash_mlx_amd import _lib
     from dflash_mlx_amd.quantize import quantize
     from dflash_mlx_amd.verify_qmm import qmm_launch
 
     dev = torch.device("cuda:0")
-    M, K, N = args.m, 4096, 4096
+    M, K, N = args.m if args.workload == "single" else 16, 4096, 4096
     per = N * K // 2 + 4 * N * K // 64
     R = max(2, math.ceil(1.0e9 / per))
     gen = torch.Generator(device=dev)
     gen.manual_seed(1)
     w_q, s, b = make_weights(torch, quantize, K, N, gen, dev)
-    pool = [(w_q.clone(), s.clone(), b.clone()) for _ in range(R)]
-    del w_q, s, b
+    pool = [(w_q, s, b)] + [(w_q.clone(), s.clone(), b.clone()) for _ in range(R - 1)]
     xg = torch.Generator(device=dev)
     xg.manual_seed(0)
     x = torch.randn((M, K), generator=xg, device=dev).to(torch.bfloat16)
@@ -318,21 +414,23 @@ def run_single(args, torch):
 
     g = graph_of(torch, fn)
     ms = time_replays(torch, g, args.steps, warmup=args.warmup)
+    del g
     us = ms * 1e3 / R
     gbs = alg_bytes(M, K, N) / (us * 1e-6) / 1e9
-    from dflash_mlx_amd import _lib
-
     name = _lib.load().dfmi_qmm_kernel_name(M, K, N, 64, 4, None).decode()
-    roofline = {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic("single", name),
-                "kernel": name, "bytes_per_launch": alg_bytes(M, K, N), "us_per_launch": round(us, 3)}
-    roofline["mfma"] = mfma_report("single", name, 2 * M * K * N, us)
-    config = {"workload": "single call [16,4096]x[4096,4096] int4 gs64, weights rotated over "
+    roofline = roofline_of("single", name, alg_bytes(M, K, N), us, 2 * M * K * N)
+    config = {"workload": f"single call [{M},4096]x[4096,4096] int4 gs64, weights rotated over "
                           f"{R} copies (1 GB)", "M": M, "K": K, "N": N}
-    return base_result(args, gbs, ms, R, config, roofline)
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline_calls(torch, [(x, w_q, s, b)], M, f"one [{M},4096]x[4096,4096] call")
+    del pool
+    return line(gbs, ms, R, config, roofline, cpu)
 
 
 def run_lmhead(args, torch):
+    import numpy as np
+
     from dflash_mlx_amd.lm_head import lm_head_greedy_accept
     from dflash_mlx_amd.quantize import quantize
 
@@ -363,21 +461,34 @@ def run_lmhead(args, torch):
 
     g = graph_of(torch, fn)
     ms_step = time_replays(torch, g, args.steps, warmup=args.warmup)  # one step = R calls
+    del g
     ms = ms_step / R
     nbytes = V * K // 2 + 4 * V * K // 64 + 2 * M * K + 12 * M
     gbs = nbytes / (ms * 1e-3) / 1e9
-    roofline = {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(gbs / HBM_PEAK_GBS, 4),
-                "traffic": measured_traffic("lmhead", "lmhead_stream_kernel"),
-                "kernel": "lmhead_stream_kernel", "bytes_per_launch": nbytes,
-                "us_per_launch": round(ms * 1e3, 3)}
-    roofline["mfma"] = mfma_report("lmhead", "lmhead_stream_kernel", 2 * M * K * V, ms * 1e3)
+    roofline = roofline_of("lmhead", "lmhead_stream_kernel", nbytes, ms * 1e3, 2 * M * K * V)
     config = {"workload": "fused lm_head [16,5120]x[151936,5120] int4 gs64 + greedy + accept",
               "M": M, "K": K, "V": V, "calls_per_step": R}
-    return base_result(args, gbs, ms_step, R, config, roofline)
+    cpu = None
+    ocpu = cpu_loaded() if not args.no_cpu else None
+    if ocpu is not None:
+        import oracle
+
+        hx, hw, hs, hb = _host16(torch, h), _host_words(w_q), _host16(torch, s), _host16(torch, b)
+        hid = ids.cpu().numpy().astype(np.int64)
+        threads = cpu_threads()
+
+        def work():
+            logits = ocpu.qmm_bf16(hx, hw, hs, hb, 64, 4, threads)
+            post = oracle.greedy_tokens_with_mask(logits, dtype="bf16")
+            oracle.verify_cycle_accept(hid, post)
+        cpu = _cpu_loop(work, nbytes, "one fused lm_head [16,5120]x[151936,5120] + greedy + accept")
+    del heads
+    return line(gbs, ms_step, R, config, roofline, cpu)
 
 
 def run_moe(args, torch):
+    import numpy as np
+
     from dflash_mlx_amd.moe import gather_qmm, gather_swiglu, moe_combine
     from dflash_mlx_amd.quantize import quantize
 
@@ -387,17 +498,15 @@ def run_moe(args, torch):
     gen.manual_seed(7)
 
     def experts(N, K):
-        wq = torch.empty((E, N, K // 8), dtype=torch.int32, device=dev)
-        sc = torch.empty((E, N, K // 64), dtype=torch.bfloat16, device=dev)
-        bi = torch.empty_like(sc)
-        for e in range(E):
-            w = torch.randn((N, K), generator=gen, device=dev) * 0.02
-            wq[e], sc[e], bi[e] = quantize(w, 64, 4, torch.bfloat16)
-        return wq, sc, bi
+        w = torch.randn((E * N, K), generator=gen, device=dev) * 0.02
+        wq, sc, bi = quantize(w, 64, 4, torch.bfloat16)
+        del w
+        return wq.reshape(E, N, K // 8), sc.reshape(E, N, K // 64), bi.reshape(E, N, K // 64)
 
     lay = []
     total = 0
     sw_bytes = dn_bytes = 0  # algorithmic bytes of the gate/up and the down launches
+    per_expert = I * D // 2 + 4 * I * D // 64
     for _ in range(layers):
         gate, up, down = experts(I, D), experts(I, D), experts(D, I)
         logits = torch.randn((T, E), generator=gen, device=dev)
@@ -412,16 +521,16 @@ def run_moe(args, torch):
         inv[order] = torch.arange(order.numel(), device=dev)
         inv = inv.to(torch.int32)  # row of each pair in the expert-sorted outputs
         n_e = int(torch.unique(flat).numel())
-        per_expert = I * D // 2 + 4 * I * D // 64
         total += n_e * 3 * per_expert + 2 * T * D * 2
         sw_bytes += n_e * 2 * per_expert + T * D * 2 + T * k * I * 2
         dn_bytes += n_e * per_expert + T * k * I * 2 + T * k * D * 2
         x = torch.randn((T, D), generator=gen, device=dev).to(torch.bfloat16)
-        lay.append((gate, up, down, rhs, lhs, inv, sc, x))
+        lay.append((gate, up, down, rhs, lhs, inv, sc, x, inds))
+    torch.cuda.synchronize()
     log(f"moe weights ready ({layers} layers)")
 
     def fn():
-        for (gate, up, down, rhs, lhs, inv, sc, x) in lay:
+        for (gate, up, down, rhs, lhs, inv, sc, x, _) in lay:
             h = gather_swiglu(x, gate, up, rhs, lhs_indices=lhs, group_size=64)
             y = gather_qmm(h, *down, rhs, group_size=64)
             moe_combine(y, sc, y_rows=inv)
@@ -434,14 +543,14 @@ def run_moe(args, torch):
     # each gather kernel's launches replayed alone (the gate/up SwiGLU pair
     # dominates: two thirds of the weight bytes)
     hs = [gather_swiglu(x, gate, up, rhs, lhs_indices=lhs, group_size=64)
-          for (gate, up, down, rhs, lhs, inv, sc, x) in lay]
+          for (gate, up, down, rhs, lhs, inv, sc, x, _) in lay]
 
     def fn_sw():
-        for (gate, up, down, rhs, lhs, inv, sc, x) in lay:
+        for (gate, up, down, rhs, lhs, inv, sc, x, _) in lay:
             gather_swiglu(x, gate, up, rhs, lhs_indices=lhs, group_size=64)
 
     def fn_dn():
-        for h, (gate, up, down, rhs, lhs, inv, sc, x) in zip(hs, lay):
+        for h, (gate, up, down, rhs, lhs, inv, sc, x, _) in zip(hs, lay):
             gather_qmm(h, *down, rhs, group_size=64)
 
     reps = max(3, args.steps // 4)
@@ -456,17 +565,42 @@ def run_moe(args, torch):
                             "bytes_per_launch": nbytes // layers,
                             "GBps": round(nbytes / (kms * 1e-3) / 1e9, 2)}
     dom = per_kernel["gather_persist_kernel"]
-    roofline = {"bound": "hbm", "achieved": dom["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(dom["GBps"] / HBM_PEAK_GBS, 4),
-                "traffic": measured_traffic("moe", "gather_persist_kernel"),
-                "kernel": "gather_persist_kernel", "bytes_per_launch": dom["bytes_per_launch"],
-                "us_per_launch": dom["us_per_launch"], "per_kernel": per_kernel}
     # algorithmic FLOP of the gate/up launch: T·k routed rows x (gate + up)
-    roofline["mfma"] = mfma_report("moe", "gather_persist_kernel", 2 * T * k * D * I * 2,
-                                   dom["us_per_launch"])
+    roofline = roofline_of("moe", "gather_persist_kernel", dom["bytes_per_launch"],
+                           dom["us_per_launch"], 2 * T * k * D * I * 2, per_kernel)
     config = {"workload": "MoE 40 layers, 16 tokens top-8 of 256 experts, hidden 2048, "
                           "expert width 512, int4 gs64", "algorithmic_bytes_per_step": total}
-    return base_result(args, gbs, ms, 3 * layers, config, roofline)
+    cpu = None
+    ocpu = cpu_loaded() if not args.no_cpu else None
+    if ocpu is not None:
+        from oracle import moe as omoe
+
+        gate, up, down, rhs, lhs, inv, sc, x, inds = lay[0]
+        hx = _host16(torch, x)
+        hi = inds.cpu().numpy()
+        hsc = sc.cpu().numpy()
+        host = {}
+        for e in np.unique(hi):
+            host[int(e)] = tuple((_host_words(t[0][e]), _host16(torch, t[1][e]),
+                                  _host16(torch, t[2][e])) for t in (gate, up, down))
+        threads = cpu_threads()
+        n_e = len(host)
+        layer_bytes = n_e * 3 * per_expert + 2 * T * D * 2
+
+        def work():
+            y = np.zeros((T * k, D), np.uint16)
+            for e, (g_, u_, d_) in host.items():
+                pairs = np.nonzero(hi.reshape(-1) == e)[0]
+                xr = hx[pairs // k]
+                gv = ocpu.qmm_bf16(xr, *g_, 64, 4, threads)
+                uv = ocpu.qmm_bf16(xr, *u_, 64, 4, threads)
+                h = omoe._silu_mul(gv, uv, "bf16")
+                y[pairs] = ocpu.qmm_bf16(h, *d_, 64, 4, threads)
+            omoe.moe_combine(y, hsc, dtype="bf16", out_dtype="bf16")
+        cpu = _cpu_loop(work, layer_bytes, f"MoE layer 0 ({n_e} distinct experts x gate/up/down "
+                                           f"+ SwiGLU + combine)")
+    del lay, hs
+    return line(gbs, ms, 3 * layers, config, roofline, cpu)
 
 
 def run_gdn(args, torch):
@@ -515,7 +649,7 @@ def run_gdn(args, torch):
     config = {"workload": "GDN rollback pair per layer: gated delta + tape over 16 steps, "
                           "replay of 9 steps; B=1, Hk=16, Hv=32, Dk=Dv=128, fp32 state, 64 layers",
               "T": T, "Hk": Hk, "Hv": Hv, "Dk": Dk, "Dv": Dv}
-    return base_result(args, gbs, ms_tape, layers, config, roofline)
+    return line(gbs, ms_tape, layers, config, roofline)
 
 
 def run_copy(args, torch):
@@ -541,13 +675,38 @@ def run_copy(args, torch):
             "bytes_written": n * 4, "ms_per_copy": round(ms, 4), "GBps_read_plus_write": round(gbs, 1)}
 
 
+def headline(args, ln):
+    """The driver's one-line contract around a workload line."""
+    out = {
+        "metric": METRIC,
+        "value": ln["value"],
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ln["ms_per_step"],
+        "us_per_call": ln["us_per_call"],
+        "pct_of_hbm_peak": ln["pct_of_hbm_peak"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights quantised int4 gs64 on GPU)",
+        "config": ln["config"],
+        "roofline": ln["roofline"],
+    }
+    if "cpu_baseline" in ln:
+        out["cpu_baseline"] = ln["cpu_baseline"]
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="9b",
-                    choices=["9b", "27b", "single", "lmhead", "moe", "gdn", "copy"])
+    ap.add_argument("--workload", default="27b",
+                    choices=["27b", "9b", "single", "lmhead", "moe", "gdn", "copy"])
     ap.add_argument("--m", type=int, default=16)
     ap.add_argument("--bits", type=int, default=4, choices=[4, 8],
                     help="weight bits of the 9b / 27b sweeps")
@@ -556,6 +715,10 @@ def main():
     ap.add_argument("--splits", type=int, default=0)
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-fuse", action="store_true",
+                    help="sweeps: one launch per matmul (no shared-activation launches)")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="default run: print the 27B line without the other configurations")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "bench.py measures one GPU only (--gpus 1); how the path "
@@ -566,9 +729,34 @@ def main():
     import __graft_entry__
 
     __graft_entry__.load_package()
-    runner = {"9b": run_sweep, "27b": run_sweep, "single": run_single, "lmhead": run_lmhead,
-              "moe": run_moe, "gdn": run_gdn, "copy": run_copy}[args.workload]
-    res = runner(args, torch)
+    wl = args.workload
+    if wl in ("27b", "9b"):
+        sweep = Sweep(torch, wl == "27b", args.bits)
+        res = headline(args, run_sweep(args, torch, sweep, args.m, f"{wl} M={args.m}",
+                                       fuse=not args.no_fuse))
+        default_run = wl == "27b" and args.m == 16 and args.bits == 4 and not args.no_configs \
+            and not (args.path or args.tiles or args.splits)
+        if default_run:
+            configs = {}
+            configs["27b_separate"] = run_sweep(args, torch, sweep, 16, "27b M=16 separate",
+                                                with_cpu=False, fuse=False)
+            for M in (8, 32):
+                configs[f"27b_m{M}"] = run_sweep(args, torch, sweep, M, f"27b M={M}")
+            del sweep
+            torch.cuda.empty_cache()
+            configs["9b"] = run_sweep(args, torch, Sweep(torch, False, 4), 16, "9b M=16")
+            torch.cuda.empty_cache()
+            configs["single"] = run_single(args, torch)
+            torch.cuda.empty_cache()
+            configs["moe"] = run_moe(args, torch)
+            torch.cuda.empty_cache()
+            configs["lmhead"] = run_lmhead(args, torch)
+            res["configs"] = configs
+    elif wl == "copy":
+        res = run_copy(args, torch)
+    else:
+        res = headline(args, {"single": run_single, "lmhead": run_lmhead, "moe": run_moe,
+                              "gdn": run_gdn}[wl](args, torch))
     print(json.dumps(res), flush=True)
 
 

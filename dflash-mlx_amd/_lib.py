@@ -29,11 +29,17 @@ _float = ctypes.c_float
 
 
 class QmmTuning(ctypes.Structure):
-    """dfmi_qmm_tuning: path (1 general, 2 streaming), tiles_per_wave,
+    """dfmi_qmm_tuning: path (1 general, 2 streaming, 3 persistent), tiles_per_wave,
     waves_per_block (general kernel K split), k_splits (streaming kernel K
     split across workgroups); 0 = automatic."""
     _fields_ = [("path", ctypes.c_int), ("tiles_per_wave", ctypes.c_int),
                 ("waves_per_block", ctypes.c_int), ("k_splits", ctypes.c_int)]
+
+
+class QmmSegment(ctypes.Structure):
+    """dfmi_qmm_segment: one matrix of a shared-activation launch."""
+    _fields_ = [("w_q", ctypes.c_void_p), ("scales", ctypes.c_void_p),
+                ("biases", ctypes.c_void_p), ("y", ctypes.c_void_p), ("N", ctypes.c_int64)]
 
 
 # name -> (restype, argtypes)
@@ -50,6 +56,12 @@ _SIGNATURES = {
                                                ctypes.POINTER(QmmTuning)]),
     "dfmi_qmm_workspace_bytes_ex": (_size, [_i64, _i64, _i64, _int, _int,
                                             ctypes.POINTER(QmmTuning)]),
+    "dfmi_qmm_affine_multi": (_int, [_c_void_p, _int, ctypes.POINTER(QmmSegment), _int, _i64,
+                                     _i64, _int, _int, _c_void_p, _size, _c_void_p]),
+    "dfmi_qmm_multi_workspace_bytes": (_size, [_i64, _i64, ctypes.POINTER(ctypes.c_int64), _int,
+                                               _int, _int]),
+    "dfmi_qmm_multi_kernel_name": (ctypes.c_char_p, [_i64, _i64, ctypes.POINTER(ctypes.c_int64),
+                                                     _int, _int, _int]),
     "dfmi_gather_qmm_affine": (_int, [_c_void_p, _int, _i64, _c_void_p, _c_void_p, _c_void_p,
                                       _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64,
                                       _int, _int, _c_void_p]),

@@ -140,54 +140,72 @@ static void launch_tag(int gs, const DensePlan& p, hipStream_t st, const DenseAr
 // no plain store is published across workgroups.
 
 constexpr size_t kCounterBytes = 65536;
+// plain calls route to the persistent kernel automatically
+constexpr bool kPersistAuto = false;
 constexpr int kMaxCounters = (int)(kCounterBytes / 4);
+constexpr int kMaxSeg = 4;  // weight matrices of one shared-activation launch
 
 struct StreamArgs {
   const uint16_t* x;
-  const uint32_t* w;
-  const uint16_t* s;
-  const uint16_t* b;
-  uint16_t* y;
-  float* partials;     // [kp][M][N] fp32 (kp > 1)
+  float* partials;     // [kp][M][pstride] fp32 (kp > 1)
   uint32_t* counters;  // [n_blocks] (kp > 1), zero between calls
-  int M, K, N;
+  int M, K;
   int chunks;
   int kp;
   int n_blocks;
   int xcd_map;
+  int pstride;  // columns of a partial row: N (one matrix) or 64 x n_blocks
 };
 
+// One weight matrix of a launch: the launch's blocks blk0 .. blk0 +
+// ceil(N / 64) - 1 are its row blocks; its partial columns are
+// 64 blk0 + row.
+struct StreamSeg {
+  const uint32_t* w;
+  const uint16_t* s;
+  const uint16_t* b;
+  uint16_t* y;
+  int N;
+  int blk0;
+};
+
+struct StreamSegs {
+  StreamSeg seg[kMaxSeg];
+  int nseg;
+};
+
+// workgroup L -> (block nb, K split kpi)
+__device__ inline void stream_unit_of(int L, int kp, int xcd_map, int& nb, int& kpi) {
+  if (xcd_map) {
+    // consecutive workgroup ids go to different XCDs (id & 7): give the kp
+    // splits of one block to one XCD so the block's partials and counter
+    // stay in one L2
+    const int xcd = L & 7, j = L >> 3;
+    const int nbl = j / kp;
+    kpi = j - nbl * kp;
+    nb = nbl * 8 + xcd;
+  } else {
+    nb = L / kp;
+    kpi = L - nb * kp;
+  }
+}
+
+// Block nb (of matrix g), K split kpi.
 template <typename Tag, int GS, int MT, int WV, int BITS, int SBPC>
-__device__ __forceinline__ void qmm_stream_body(StreamArgs a) {
+__device__ __forceinline__ void qmm_stream_body(const StreamArgs& a, const StreamSeg& g, int nb,
+                                                int kpi) {
   using S = Stream<Tag, GS, MT, WV, SBPC, BITS>;
   constexpr int kThreads = 64 * WV;
-  int nb, kpi;
-  {
-    const int L = blockIdx.x;
-    if (a.xcd_map) {
-      // consecutive workgroup ids go to different XCDs (id & 7): give the
-      // kp splits of one block to one XCD so the block's partials and
-      // counter stay in one L2
-      const int xcd = L & 7, j = L >> 3;
-      const int nbl = j / a.kp;
-      kpi = j - nbl * a.kp;
-      nb = nbl * 8 + xcd;
-    } else {
-      nb = L / a.kp;
-      kpi = L - nb * a.kp;
-    }
-  }
-  if (nb >= a.n_blocks) return;  // uniform, before any barrier
   typename S::Ctx cx;
   cx.x = buffer_rsrc(a.x, (uint32_t)a.M * (uint32_t)a.K * 2u);
-  cx.w = buffer_rsrc(a.w, (uint32_t)a.N * (uint32_t)(a.K / 8 * BITS));
-  cx.s = buffer_rsrc(a.s, (uint32_t)a.N * (uint32_t)(a.K / GS) * 2u);
-  cx.b = buffer_rsrc(a.b, (uint32_t)a.N * (uint32_t)(a.K / GS) * 2u);
+  cx.w = buffer_rsrc(g.w, (uint32_t)g.N * (uint32_t)(a.K / 8 * BITS));
+  cx.s = buffer_rsrc(g.s, (uint32_t)g.N * (uint32_t)(a.K / GS) * 2u);
+  cx.b = buffer_rsrc(g.b, (uint32_t)g.N * (uint32_t)(a.K / GS) * 2u);
   cx.K = a.K;
   cx.M = a.M;
-  cx.N = a.N;
+  cx.N = g.N;
   cx.groups = a.K / GS;
-  cx.n0 = nb * S::NB;
+  cx.n0 = (nb - g.blk0) * S::NB;
   cx.lane = threadIdx.x & 63;
   cx.wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   cx.dense();
@@ -231,14 +249,15 @@ __device__ __forceinline__ void qmm_stream_body(StreamArgs a) {
   if (a.kp == 1) {
 #pragma unroll
     for (int q = 0; q < PER; ++q)
-      if (mi[q] < a.M && ni[q] < a.N) a.y[(int64_t)mi[q] * a.N + ni[q]] = Num<Tag>::f2h(v[q]);
+      if (mi[q] < a.M && ni[q] < g.N) g.y[(int64_t)mi[q] * g.N + ni[q]] = Num<Tag>::f2h(v[q]);
     return;
   }
-  float* part = a.partials + (int64_t)kpi * a.M * a.N;
+  // this matrix's partial columns start at 64 blk0
+  float* part = a.partials + (int64_t)kpi * a.M * a.pstride + (int64_t)g.blk0 * S::NB;
 #pragma unroll
   for (int q = 0; q < PER; ++q)
-    if (mi[q] < a.M && ni[q] < a.N)
-      __hip_atomic_store(part + (int64_t)mi[q] * a.N + ni[q], v[q], __ATOMIC_RELAXED,
+    if (mi[q] < a.M && ni[q] < g.N)
+      __hip_atomic_store(part + (int64_t)mi[q] * a.pstride + ni[q], v[q], __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
   int* s_last = reinterpret_cast<int*>(dfmi_smem);  // red[0], already consumed
   stage_barrier<0>();  // every partial store of the workgroup has completed
@@ -258,10 +277,10 @@ __device__ __forceinline__ void qmm_stream_body(StreamArgs a) {
 #pragma unroll
   for (int q = 0; q < PER; ++q) {
     sum[q] = 0.f;
-    ok[q] = mi[q] < a.M && ni[q] < a.N;
-    off[q] = ok[q] ? (int64_t)mi[q] * a.N + ni[q] : 0;
+    ok[q] = mi[q] < a.M && ni[q] < g.N;
+    off[q] = ok[q] ? (int64_t)mi[q] * a.pstride + (int64_t)g.blk0 * S::NB + ni[q] : 0;
   }
-  const int64_t split = (int64_t)a.M * a.N;
+  const int64_t split = (int64_t)a.M * a.pstride;
   for (int q0 = 0; q0 < a.kp; q0 += 4) {
     // unconditional loads (a split past kp re-reads the last one and is
     // dropped), so the block is straight-line code with one wait
@@ -281,7 +300,7 @@ __device__ __forceinline__ void qmm_stream_body(StreamArgs a) {
   }
 #pragma unroll
   for (int q = 0; q < PER; ++q)
-    if (ok[q]) a.y[(int64_t)mi[q] * a.N + ni[q]] = Num<Tag>::f2h(sum[q]);
+    if (ok[q]) g.y[(int64_t)mi[q] * g.N + ni[q]] = Num<Tag>::f2h(sum[q]);
   if (threadIdx.x == 0)
     __hip_atomic_exchange(&a.counters[nb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -359,49 +378,82 @@ __global__ __launch_bounds__(64 * WV) void qmm_stream_kernel(
     const uint16_t* x, const uint32_t* w, const uint16_t* s, const uint16_t* b, uint16_t* y,
     float* partials, uint32_t* counters, int M, int K, int N, int chunks, int kp, int n_blocks,
     int xcd_map) {
+  int nb, kpi;
+  stream_unit_of(blockIdx.x, kp, xcd_map, nb, kpi);
+  if (nb >= n_blocks) return;  // uniform, before any barrier
   qmm_stream_body<Tag, GS, MT, WV, BITS, SBPC>(
-      StreamArgs{x, w, s, b, y, partials, counters, M, K, N, chunks, kp, n_blocks, xcd_map});
+      StreamArgs{x, partials, counters, M, K, chunks, kp, n_blocks, xcd_map, N},
+      StreamSeg{w, s, b, y, N, 0}, nb, kpi);
+}
+
+// Several weight matrices over the same activations (q / k / v, gate / up):
+// their row blocks form one grid.
+template <typename Tag, int GS, int MT, int WV, int BITS, int SBPC>
+__global__ __launch_bounds__(64 * WV) void qmm_stream_multi_kernel(StreamArgs a, StreamSegs m) {
+  int nb, kpi;
+  stream_unit_of(blockIdx.x, a.kp, a.xcd_map, nb, kpi);
+  if (nb >= a.n_blocks) return;  // uniform, before any barrier
+  // the matrix holding block nb (constant indices: the table stays in SGPRs)
+  StreamSeg g = m.seg[0];
+#pragma unroll
+  for (int i = 1; i < kMaxSeg; ++i)
+    if (i < m.nseg && nb >= m.seg[i].blk0) g = m.seg[i];
+  qmm_stream_body<Tag, GS, MT, WV, BITS, SBPC>(a, g, nb, kpi);
 }
 
 template <typename Tag, int GS, int MT, int WV, int BITS>
-static void launch_stream_t(const StreamPlan& p, hipStream_t st, const StreamArgs& a) {
+static void launch_stream_t(const StreamPlan& p, hipStream_t st, const StreamArgs& a,
+                            const StreamSegs& m) {
   constexpr int SBPC = BITS == 8 && WV == 8 ? 8 : kSbPieces;  // = stream_sb_pieces(BITS, WV)
   const int lds = Stream<Tag, GS, MT, WV, SBPC, BITS>::LDS_BYTES;
-  hipLaunchKernelGGL((qmm_stream_kernel<Tag, GS, MT, WV, BITS, SBPC>), dim3(p.grid_x),
-                     dim3(64 * WV), lds, st, a.x, a.w, a.s, a.b, a.y, a.partials, a.counters,
-                     a.M, a.K, a.N, a.chunks, a.kp, a.n_blocks, a.xcd_map);
+  if (m.nseg == 1) {
+    const StreamSeg& g = m.seg[0];
+    hipLaunchKernelGGL((qmm_stream_kernel<Tag, GS, MT, WV, BITS, SBPC>), dim3(p.grid_x),
+                       dim3(64 * WV), lds, st, a.x, g.w, g.s, g.b, g.y, a.partials, a.counters,
+                       a.M, a.K, g.N, a.chunks, a.kp, a.n_blocks, a.xcd_map);
+  } else {
+    hipLaunchKernelGGL((qmm_stream_multi_kernel<Tag, GS, MT, WV, BITS, SBPC>), dim3(p.grid_x),
+                       dim3(64 * WV), lds, st, a, m);
+  }
 }
 
 template <typename Tag, int GS, int BITS>
-static void launch_stream_bits(const StreamPlan& p, hipStream_t st, const StreamArgs& a) {
+static void launch_stream_bits(const StreamPlan& p, hipStream_t st, const StreamArgs& a,
+                               const StreamSegs& m) {
   if (p.MT == 1) {
-    if (p.WV == 8) launch_stream_t<Tag, GS, 1, 8, BITS>(p, st, a);
-    else launch_stream_t<Tag, GS, 1, 4, BITS>(p, st, a);
+    if (p.WV == 8) launch_stream_t<Tag, GS, 1, 8, BITS>(p, st, a, m);
+    else launch_stream_t<Tag, GS, 1, 4, BITS>(p, st, a, m);
   } else {
-    launch_stream_t<Tag, GS, 2, 4, BITS>(p, st, a);
+    launch_stream_t<Tag, GS, 2, 4, BITS>(p, st, a, m);
   }
 }
 
 template <typename Tag, int GS>
-static void launch_stream_gs(const StreamPlan& p, hipStream_t st, const StreamArgs& a) {
-  if (p.bits == 8) launch_stream_bits<Tag, GS, 8>(p, st, a);
-  else launch_stream_bits<Tag, GS, 4>(p, st, a);
+static void launch_stream_gs(const StreamPlan& p, hipStream_t st, const StreamArgs& a,
+                             const StreamSegs& m) {
+  if (p.bits == 8) launch_stream_bits<Tag, GS, 8>(p, st, a, m);
+  else launch_stream_bits<Tag, GS, 4>(p, st, a, m);
 }
 
 template <typename Tag>
-static void launch_stream(int gs, const StreamPlan& p, hipStream_t st, const StreamArgs& a) {
-  if (gs == 32) launch_stream_gs<Tag, 32>(p, st, a);
-  else if (gs == 64) launch_stream_gs<Tag, 64>(p, st, a);
-  else launch_stream_gs<Tag, 128>(p, st, a);
+static void launch_stream(int gs, const StreamPlan& p, hipStream_t st, const StreamArgs& a,
+                          const StreamSegs& m) {
+  if (gs == 32) launch_stream_gs<Tag, 32>(p, st, a, m);
+  else if (gs == 64) launch_stream_gs<Tag, 64>(p, st, a, m);
+  else launch_stream_gs<Tag, 128>(p, st, a, m);
 }
 
 // Dynamic LDS above 64 KiB needs the per-kernel attribute raised once.
 template <typename Tag, int GS, int MT, int WV, int BITS>
 static void allow_lds_t() {
   constexpr int SBPC = BITS == 8 && WV == 8 ? 8 : kSbPieces;
+  constexpr int lds = Stream<Tag, GS, MT, WV, SBPC, BITS>::LDS_BYTES;
   (void)hipFuncSetAttribute(
       reinterpret_cast<const void*>(&qmm_stream_kernel<Tag, GS, MT, WV, BITS, SBPC>),
-      hipFuncAttributeMaxDynamicSharedMemorySize, Stream<Tag, GS, MT, WV, SBPC, BITS>::LDS_BYTES);
+      hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  (void)hipFuncSetAttribute(
+      reinterpret_cast<const void*>(&qmm_stream_multi_kernel<Tag, GS, MT, WV, BITS, SBPC>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, lds);
 }
 
 template <typename Tag, int GS>
@@ -475,9 +527,73 @@ static bool use_stream(int64_t M, int64_t K, int64_t N, int gs, int bits,
          ((N + kStreamRows - 1) / kStreamRows <= kMaxCounters || K / gs <= sb_max_groups(sbpc));
 }
 
-// tuning.path: 0 automatic, 1 general kernel, 2 streaming kernel
+// tuning.path: 0 automatic, 1 general kernel, 2 streaming kernel, 3 persistent
+// streaming kernel
 static bool valid_path(const dfmi_qmm_tuning* tune) {
-  return !tune || (tune->path >= 0 && tune->path <= 2);
+  return !tune || (tune->path >= 0 && tune->path <= 3);
+}
+
+// The persistent streaming kernel takes a plain call when the automatic
+// choice (or path 3) asks for it and its planner accepts the shape.  The
+// automatic choice uses it for every shape it takes (it measured faster than
+// the per-call streaming grid on every M = 16 verify shape).
+static bool use_persist(int64_t M, int64_t K, int64_t N, int gs, int bits,
+                        const dfmi_qmm_tuning* tune, size_t* ws) {
+  const int path = tune ? tune->path : 0;
+  if (path != 0 && path != 3) return false;
+  if (path == 0 && tune && (tune->k_splits || tune->waves_per_block || tune->tiles_per_wave))
+    return false;  // explicit split / wave choices address the per-call grid
+  if (path == 0 && !kPersistAuto) return false;
+  return dfmi_persist_plan(M, K, &N, 1, gs, bits, ws);
+}
+
+// The streaming kernel over the matrices of m (their row blocks one grid of
+// n_cols / 64 blocks), after the caller's argument checks.
+static int launch_streaming(const void* x, int x_dtype, const StreamSegs& m, int64_t M, int64_t K,
+                            int64_t n_cols, int gs, int bits, const dfmi_qmm_tuning* tuning,
+                            void* workspace, size_t workspace_bytes, hipStream_t st) {
+  StreamPlan p;
+  const int rc = plan_stream(M, K, n_cols, gs, bits, tuning, p);
+  if (rc != DFMI_OK) return rc;
+  StreamArgs a;
+  a.x = static_cast<const uint16_t*>(x);
+  a.partials = nullptr;
+  a.counters = nullptr;
+  if (p.kp > 1) {
+    if (!workspace || workspace_bytes < p.ws_bytes || !aligned16(workspace)) {
+      set_error("dfmi_qmm: workspace of %zu bytes (16-byte aligned) required, got %zu",
+                p.ws_bytes, workspace_bytes);
+      return DFMI_ENOSPC;
+    }
+    a.counters = static_cast<uint32_t*>(workspace);
+    a.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
+  }
+  a.M = (int)M;
+  a.K = (int)K;
+  a.chunks = p.chunks;
+  a.kp = p.kp;
+  a.n_blocks = p.n_blocks;
+  a.xcd_map = p.xcd_map;
+  a.pstride = (int)n_cols;
+  allow_lds_all();
+  if (x_dtype == DFMI_BF16) launch_stream<BF16>(gs, p, st, a, m);
+  else launch_stream<F16>(gs, p, st, a, m);
+  return check_launch(m.nseg == 1 ? "dfmi_qmm_affine" : "dfmi_qmm_affine_multi");
+}
+
+// Shared-activation launches take the streaming kernel when every matrix
+// does (their blocks then form one grid); the columns of that grid, 64 per
+// block, or 0.
+static int64_t multi_stream_cols(int64_t M, int64_t K, const int64_t* Ns, int nseg, int gs,
+                                 int bits) {
+  int64_t blocks = 0;
+  for (int i = 0; i < nseg; ++i) {
+    if (!use_stream(M, K, Ns[i], gs, bits, nullptr)) return 0;
+    blocks += (Ns[i] + kStreamRows - 1) / kStreamRows;
+  }
+  if (blocks > kMaxCounters && K / gs > sb_max_groups(bits == 8 ? 8 : kSbPieces)) return 0;
+  if (blocks * kStreamRows >= (1ll << 31) / 32) return 0;
+  return blocks * kStreamRows;
 }
 
 extern "C" size_t dfmi_qmm_workspace_bytes_ex(int64_t M, int64_t K, int64_t N, int group_size,
@@ -485,6 +601,8 @@ extern "C" size_t dfmi_qmm_workspace_bytes_ex(int64_t M, int64_t K, int64_t N, i
   if (validate_qmm(DFMI_BF16, M, K, N, group_size, bits) != DFMI_OK || M == 0 || N == 0 ||
       !valid_path(tuning))
     return 0;
+  size_t pws = 0;
+  if (use_persist(M, K, N, group_size, bits, tuning, &pws)) return pws;
   if (!use_stream(M, K, N, group_size, bits, tuning)) return 0;
   StreamPlan p;
   if (plan_stream(M, K, N, group_size, bits, tuning, p) != DFMI_OK) return 0;
@@ -495,6 +613,8 @@ extern "C" const char* dfmi_qmm_kernel_name(int64_t M, int64_t K, int64_t N, int
                                              int bits, const dfmi_qmm_tuning* tuning) {
   if (validate_qmm(DFMI_BF16, M, K, N, group_size, bits) != DFMI_OK || !valid_path(tuning))
     return nullptr;
+  if (use_persist(M, K, N, group_size, bits, tuning, nullptr)) return "qmm_persist_kernel";
+  if (tuning && tuning->path == 3) return nullptr;
   if (bits == 8) return use_stream(M, K, N, group_size, bits, tuning) ? "qmm8_stream_kernel"
                                                                       : "qmm8_kernel";
   return use_stream(M, K, N, group_size, bits, tuning) ? "qmm_stream_kernel" : "qmm_dense_kernel";
@@ -525,6 +645,13 @@ extern "C" int dfmi_qmm_affine_ex(const void* x, int x_dtype, const uint32_t* w_
               (long long)M, (long long)K, (long long)N, group_size, bits);
     return DFMI_EINVAL;
   }
+  size_t pws = 0;
+  const bool persist = use_persist(M, K, N, group_size, bits, tuning, &pws);
+  if (tuning && tuning->path == 3 && !persist) {
+    set_error("dfmi_qmm: shape M=%lld K=%lld N=%lld gs=%d bits=%d outside the persistent kernel",
+              (long long)M, (long long)K, (long long)N, group_size, bits);
+    return DFMI_EINVAL;
+  }
   if (!x || !w_q || !scales || !biases || !y) {
     set_error("dfmi_qmm: null pointer");
     return DFMI_EINVAL;
@@ -533,42 +660,22 @@ extern "C" int dfmi_qmm_affine_ex(const void* x, int x_dtype, const uint32_t* w_
     set_error("dfmi_qmm: x, w_q, scales and biases must be 16-byte aligned");
     return DFMI_EINVAL;
   }
+  if (persist) {
+    const dfmi_qmm_segment seg{w_q, scales, biases, y, N};
+    return dfmi_persist_launch(x, x_dtype, &seg, 1, M, K, group_size, workspace,
+                               workspace_bytes, stream);
+  }
   hipStream_t st = static_cast<hipStream_t>(stream);
   // 8-bit: the streaming kernel where it applies, else the register-load kernel
   if (bits == 8 && !use_stream(M, K, N, group_size, bits, tuning))
     return dfmi_qmm8_launch(x, x_dtype, w_q, scales, biases, y, M, K, N, group_size, stream);
   if (use_stream(M, K, N, group_size, bits, tuning)) {
-    StreamPlan p;
-    rc = plan_stream(M, K, N, group_size, bits, tuning, p);
-    if (rc != DFMI_OK) return rc;
-    StreamArgs a;
-    a.x = static_cast<const uint16_t*>(x);
-    a.w = w_q;
-    a.s = static_cast<const uint16_t*>(scales);
-    a.b = static_cast<const uint16_t*>(biases);
-    a.y = static_cast<uint16_t*>(y);
-    a.partials = nullptr;
-    a.counters = nullptr;
-    if (p.kp > 1) {
-      if (!workspace || workspace_bytes < p.ws_bytes || !aligned16(workspace)) {
-        set_error("dfmi_qmm: workspace of %zu bytes (16-byte aligned) required, got %zu",
-                  p.ws_bytes, workspace_bytes);
-        return DFMI_ENOSPC;
-      }
-      a.counters = static_cast<uint32_t*>(workspace);
-      a.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
-    }
-    a.M = (int)M;
-    a.K = (int)K;
-    a.N = (int)N;
-    a.chunks = p.chunks;
-    a.kp = p.kp;
-    a.n_blocks = p.n_blocks;
-    a.xcd_map = p.xcd_map;
-    allow_lds_all();
-    if (x_dtype == DFMI_BF16) launch_stream<BF16>(group_size, p, st, a);
-    else launch_stream<F16>(group_size, p, st, a);
-    return check_launch("dfmi_qmm_affine");
+    StreamSegs m{};
+    m.seg[0] = StreamSeg{w_q, static_cast<const uint16_t*>(scales),
+                         static_cast<const uint16_t*>(biases), static_cast<uint16_t*>(y), (int)N, 0};
+    m.nseg = 1;
+    return launch_streaming(x, x_dtype, m, M, K, N, group_size, bits, tuning, workspace,
+                            workspace_bytes, st);
   }
   DensePlan p;
   rc = plan_dense(M, K, N, tuning, p);
@@ -594,4 +701,83 @@ extern "C" int dfmi_qmm_affine(const void* x, int x_dtype, const uint32_t* w_q, 
                                void* stream) {
   return dfmi_qmm_affine_ex(x, x_dtype, w_q, scales, biases, y, M, K, N, group_size, bits,
                             workspace, workspace_bytes, nullptr, stream);
+}
+
+extern "C" size_t dfmi_qmm_multi_workspace_bytes(int64_t M, int64_t K, const int64_t* Ns,
+                                                 int nseg, int group_size, int bits) {
+  if (!Ns || nseg < 1 || nseg > kMaxSeg) return 0;
+  for (int i = 0; i < nseg; ++i)
+    if (validate_qmm(DFMI_BF16, M, K, Ns[i], group_size, bits) != DFMI_OK) return 0;
+  if (M == 0) return 0;
+  const int64_t cols = multi_stream_cols(M, K, Ns, nseg, group_size, bits);
+  if (cols > 0) {
+    StreamPlan p;
+    return plan_stream(M, K, cols, group_size, bits, nullptr, p) == DFMI_OK ? p.ws_bytes : 0;
+  }
+  size_t ws = 0;
+  for (int i = 0; i < nseg; ++i)
+    ws = std::max(ws, dfmi_qmm_workspace_bytes_ex(M, K, Ns[i], group_size, bits, nullptr));
+  return ws;
+}
+
+extern "C" const char* dfmi_qmm_multi_kernel_name(int64_t M, int64_t K, const int64_t* Ns,
+                                                   int nseg, int group_size, int bits) {
+  if (!Ns || nseg < 1 || nseg > kMaxSeg) return nullptr;
+  for (int i = 0; i < nseg; ++i)
+    if (validate_qmm(DFMI_BF16, M, K, Ns[i], group_size, bits) != DFMI_OK) return nullptr;
+  if (multi_stream_cols(M, K, Ns, nseg, group_size, bits) <= 0) return nullptr;
+  return nseg == 1 ? "qmm_stream_kernel" : "qmm_stream_multi_kernel";
+}
+
+extern "C" int dfmi_qmm_affine_multi(const void* x, int x_dtype, const dfmi_qmm_segment* segs,
+                                     int nseg, int64_t M, int64_t K, int group_size, int bits,
+                                     void* workspace, size_t workspace_bytes, void* stream) {
+  if (!segs || nseg < 1 || nseg > kMaxSeg) {
+    set_error("dfmi_qmm_multi: 1..%d segments required (got %d)", kMaxSeg, nseg);
+    return DFMI_EINVAL;
+  }
+  int64_t Ns[kMaxSeg];
+  for (int i = 0; i < nseg; ++i) {
+    const int rc = validate_qmm(x_dtype, M, K, segs[i].N, group_size, bits);
+    if (rc != DFMI_OK) return rc;
+    Ns[i] = segs[i].N;
+  }
+  if (M == 0) return DFMI_OK;
+  if (!x || !aligned16(x)) {
+    set_error("dfmi_qmm_multi: x must be a 16-byte aligned device pointer");
+    return DFMI_EINVAL;
+  }
+  for (int i = 0; i < nseg; ++i) {
+    if (segs[i].N == 0) continue;  // nothing of an empty matrix is read or written
+    if (!segs[i].w_q || !segs[i].scales || !segs[i].biases || !segs[i].y) {
+      set_error("dfmi_qmm_multi: null pointer in segment %d", i);
+      return DFMI_EINVAL;
+    }
+    if (!aligned16(segs[i].w_q) || !aligned16(segs[i].scales) || !aligned16(segs[i].biases)) {
+      set_error("dfmi_qmm_multi: segment %d: w_q, scales and biases must be 16-byte aligned", i);
+      return DFMI_EINVAL;
+    }
+  }
+  const int64_t cols = multi_stream_cols(M, K, Ns, nseg, group_size, bits);
+  if (cols > 0) {
+    StreamSegs m{};
+    int blk = 0;
+    for (int i = 0; i < nseg; ++i) {
+      m.seg[i] = StreamSeg{segs[i].w_q, static_cast<const uint16_t*>(segs[i].scales),
+                           static_cast<const uint16_t*>(segs[i].biases),
+                           static_cast<uint16_t*>(segs[i].y), (int)Ns[i], blk};
+      blk += (int)((Ns[i] + kStreamRows - 1) / kStreamRows);
+    }
+    m.nseg = nseg;
+    return launch_streaming(x, x_dtype, m, M, K, cols, group_size, bits, nullptr, workspace,
+                            workspace_bytes, static_cast<hipStream_t>(stream));
+  }
+  // one launch per matrix, in order on the stream (they may share the workspace)
+  for (int i = 0; i < nseg; ++i) {
+    const int rc = dfmi_qmm_affine_ex(x, x_dtype, segs[i].w_q, segs[i].scales, segs[i].biases,
+                                      segs[i].y, M, K, segs[i].N, group_size, bits, workspace,
+                                      workspace_bytes, nullptr, stream);
+    if (rc != DFMI_OK) return rc;
+  }
+  return DFMI_OK;
 }

@@ -27,6 +27,7 @@ from .quantize import quantize
 from .verify_qmm import (
     _kparts_tuning,
     _m4_ksplit_np_shape,
+    qmm_multi_launch,
     _resolve_m16_ktmpl_variant,
     qmm_launch,
     quantized_matmul,
@@ -180,13 +181,19 @@ def _build_dispatch(obj: VerifyQuantizedLinear, *, enable_qmm: Optional[bool] = 
         b_c = _runtime.aligned_contiguous(obj.biases)
         kernel_dtypes = (torch.bfloat16, torch.float16)
 
+        object.__setattr__(obj, "_packed", (w_c, s_c, b_c))
+
         def call(x: torch.Tensor) -> torch.Tensor:
             orig = x.shape
             m = math.prod(int(d) for d in orig[:-1])
             if x.dtype in kernel_dtypes and ((m == 16 and m16_qmm) or (m == 4 and m4_qmm)):
-                x2 = _runtime.aligned_contiguous(x.reshape(m, orig[-1]))
-                tuning = m16_tuning if m == 16 else None
-                y = qmm_launch(x2, w_c, s_c, b_c, N, gs, bits, tuning).reshape(*orig[:-1], N)
+                sib = obj.__dict__.get("_sibling")
+                if sib is not None:
+                    y = sib[0].product(sib[1], x, m).reshape(*orig[:-1], N)
+                else:
+                    x2 = _runtime.aligned_contiguous(x.reshape(m, orig[-1]))
+                    tuning = m16_tuning if m == 16 else None
+                    y = qmm_launch(x2, w_c, s_c, b_c, N, gs, bits, tuning).reshape(*orig[:-1], N)
             else:
                 y = _stock(x)
             return y + bias if bias is not None else y
@@ -244,11 +251,78 @@ def prewarm_verify_kernels(model: nn.Module, *, input_dtype: torch.dtype = torch
     return warmed
 
 
+# Sibling projections that read the same input in the decoder layers the
+# reference targets (q/k/v of self_attn, gate/up of mlp).
+_SIBLING_SETS = (("q_proj", "k_proj", "v_proj"), ("gate_proj", "up_proj"))
+
+
+class SiblingGroup:
+    """Verify modules of one parent that read the same input: the first member
+    called with a verify-sized input computes every member's product in one
+    ``dfmi_qmm_affine_multi`` launch; the others return theirs when they are
+    called with the same tensor (same storage, version, shape, strides and
+    stream) -- in the model's call order, with no change to the model code.
+    A member called with any other input recomputes the group."""
+
+    def __init__(self, members):
+        self.members = list(members)
+        self._key = None
+        self._ys = None
+        self._taken: set[int] = set()
+
+    def product(self, idx: int, x: torch.Tensor, m: int) -> torch.Tensor:
+        key = (x.data_ptr(), x._version, tuple(x.shape), tuple(x.stride()), x.dtype,
+               _runtime.stream_ptr(x.device))
+        if self._ys is not None and self._key == key and idx not in self._taken:
+            y = self._ys[idx]
+        else:
+            x2 = _runtime.aligned_contiguous(x.reshape(m, int(x.shape[-1])))
+            first = self.members[0]
+            self._ys = qmm_multi_launch(x2, [mem._packed for mem in self.members],
+                                        first.group_size, first.bits)
+            self._key = key
+            self._taken = set()
+            y = self._ys[idx]
+        self._taken.add(idx)
+        if len(self._taken) == len(self.members):
+            self._key, self._ys, self._taken = None, None, set()  # drop the references
+        return y
+
+
+def _group_siblings(model: nn.Module) -> int:
+    """Attach a SiblingGroup to each set of sibling verify modules of one
+    parent that share K, bits, group size and scale dtype and take the verify
+    kernels; returns the number of groups."""
+    groups = 0
+    for _, parent in model.named_modules():
+        for names in _SIBLING_SETS:
+            mods = [getattr(parent, n, None) for n in names]
+            if not all(isinstance(m, VerifyQuantizedLinear) and "_packed" in m.__dict__
+                       for m in mods):
+                continue
+            sig = {(int(m.weight.shape[1]) * (32 // m.bits), m.bits, m.group_size, m.scales.dtype)
+                   for m in mods}
+            if len(sig) != 1:
+                continue
+            grp = SiblingGroup(mods)
+            for i, m in enumerate(mods):
+                object.__setattr__(m, "_sibling", (grp, i))
+            groups += 1
+    return groups
+
+
 def install_verify_linears(model: nn.Module, *,
                            predicate: Optional[Callable[[str, QuantizedLinear], bool]] = None,
-                           enable_qmm: Optional[bool] = None) -> int:
+                           enable_qmm: Optional[bool] = None,
+                           fuse_siblings: bool = False) -> int:
     """dflash_mlx/verify_linear.py:338-361: swap eligible QuantizedLinear
-    leaves for VerifyQuantizedLinear; returns the number swapped."""
+    leaves for VerifyQuantizedLinear; returns the number swapped.
+
+    ``fuse_siblings`` (no reference counterpart, opt-in): group q/k/v and
+    gate/up siblings so each set runs as one shared-activation launch
+    (:class:`SiblingGroup`); every member's output equals what
+    ``quantized_matmul_multi`` returns for it (plus its bias), which is
+    within fp32 summation order of the member's own launch."""
     if predicate is None:
         predicate = lambda path, m: is_verify_eligible(m, path=path)  # noqa: E731
     count = 0
@@ -258,11 +332,14 @@ def install_verify_linears(model: nn.Module, *,
         if isinstance(m, QuantizedLinear) and predicate(path, m):
             _set_module(model, path, VerifyQuantizedLinear.from_quantized(m, enable_qmm=enable_qmm))
             count += 1
+    if fuse_siblings:
+        _group_siblings(model)
     return count
 
 
 __all__ = [
     "QuantizedLinear",
+    "SiblingGroup",
     "VerifyQuantizedLinear",
     "install_verify_linears",
     "is_verify_eligible",

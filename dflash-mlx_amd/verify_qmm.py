@@ -125,6 +125,34 @@ def qmm_launch(x2: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: 
     return y
 
 
+def qmm_multi_launch(x2: torch.Tensor, mats, group_size: int, bits: int,
+                     outs=None) -> list:
+    """One ``dfmi_qmm_affine_multi`` launch on the current stream: the
+    matrices ``mats = [(w, scales, biases), ...]`` (1..4) share ``x2 [M, K]``;
+    returns ``[y_i [M, N_i]]``."""
+    lib = _lib.load()
+    M, K = int(x2.shape[0]), int(x2.shape[1])
+    dev = x2.device
+    n = len(mats)
+    if not 1 <= n <= 4:
+        raise ValueError("1..4 matrices per launch")
+    Ns = [int(w.shape[0]) for (w, _, _) in mats]
+    ys = outs if outs is not None else [torch.empty((M, N), dtype=x2.dtype, device=dev)
+                                        for N in Ns]
+    segs = (_lib.QmmSegment * n)()
+    for i, ((w, sc, bi), y) in enumerate(zip(mats, ys)):
+        segs[i].w_q, segs[i].scales, segs[i].biases = w.data_ptr(), sc.data_ptr(), bi.data_ptr()
+        segs[i].y, segs[i].N = y.data_ptr(), Ns[i]
+    ns = (ctypes.c_int64 * n)(*Ns)
+    need = int(lib.dfmi_qmm_multi_workspace_bytes(M, K, ns, n, int(group_size), int(bits)))
+    ws, ws_bytes = _runtime.workspace(dev, need) if need else (0, 0)
+    status = lib.dfmi_qmm_affine_multi(x2.data_ptr(), _runtime.dtype_code(x2.dtype), segs, n, M,
+                                       K, int(group_size), int(bits), ws, ws_bytes,
+                                       _runtime.stream_ptr(dev))
+    _lib.check(status, "dfmi_qmm_affine_multi")
+    return ys
+
+
 def _prepare(x, w, scales, biases):
     for t, name in ((x, "x"), (w, "w"), (scales, "scales"), (biases, "biases")):
         _runtime.require_device(t, name)
@@ -157,6 +185,24 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
     N = int(wq.shape[0])
     y = qmm_launch(x2, wq, s, b, N, group_size, bits, tuning)
     return y.reshape(*x.shape[:-1], N)
+
+
+def quantized_matmul_multi(x: torch.Tensor, weights, *, group_size: int = 64,
+                           bits: int = 4) -> list:
+    """``[x . dequant(W_i)^T for W_i in weights]`` in one launch, for sibling
+    projections that read the same input (q/k/v, gate/up).  ``weights`` is a
+    list of 1..4 ``(w, scales, biases)``; the reference calls ``verify_matmul``
+    once per projection (dflash_mlx/verify_linear.py:266-286).  Each result is
+    within fp32 summation order of :func:`quantized_matmul` on that matrix."""
+    if x.dtype not in _KERNEL_DTYPES:
+        raise _lib.DfmiUnsupported(_lib.DFMI_EINVAL, f"x dtype {x.dtype} unsupported")
+    mats = []
+    x2 = None
+    for (w, scales, biases) in weights:
+        x2, wq, s, b, M, K = _prepare(x, w, scales, biases)
+        mats.append((wq, s, b))
+    ys = qmm_multi_launch(x2, mats, group_size, bits)
+    return [y.reshape(*x.shape[:-1], int(y.shape[-1])) for y in ys]
 
 
 def _should_use_verify(x: torch.Tensor, group_size: int, bits: int, transpose: bool) -> bool:

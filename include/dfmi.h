@@ -50,7 +50,10 @@ const char *dfmi_last_error(void);
  * fields mean "automatic".
  *   path: 1 = general kernel, 2 = streaming kernel (DFMI_EINVAL if the shape
  *         is outside it: M <= 32, K % 256 == 0, K % (8*group_size) == 0;
- *         checked for both weight widths); any other value is DFMI_EINVAL;
+ *         checked for both weight widths), 3 = persistent stream-K kernel
+ *         (DFMI_EINVAL outside M <= 16, int4, K % 256 == 0, K >= 512, K a
+ *         multiple of 8 groups, and its planner); any other value is
+ *         DFMI_EINVAL;
  *   tiles_per_wave: general kernel, 16-row weight tiles per wavefront (1, 2,
  *         4); the streaming kernel always covers 64 rows per workgroup;
  *   waves_per_block: general kernel, wavefronts of a workgroup that split K
@@ -99,13 +102,52 @@ int dfmi_qmm_affine_ex(const void *x, int x_dtype, const uint32_t *w_q, const vo
 size_t dfmi_qmm_workspace_bytes(int64_t M, int64_t K, int64_t N, int group_size, int bits);
 /* Host-only plan query (no reference counterpart; for benchmarks and
  * profiles): name of the kernel dfmi_qmm_affine_ex would launch for this
- * shape, "qmm_stream_kernel", "qmm_dense_kernel" or (bits 8)
- * "qmm8_stream_kernel" / "qmm8_kernel";
+ * shape, "qmm_persist_kernel", "qmm_stream_kernel", "qmm_dense_kernel" or
+ * (bits 8) "qmm8_stream_kernel" / "qmm8_kernel";
  * NULL if unsupported. */
 const char *dfmi_qmm_kernel_name(int64_t M, int64_t K, int64_t N, int group_size, int bits,
                                  const dfmi_qmm_tuning *tuning);
 size_t dfmi_qmm_workspace_bytes_ex(int64_t M, int64_t K, int64_t N, int group_size, int bits,
                                    const dfmi_qmm_tuning *tuning);
+
+/*
+ * Several matmuls that share their activations, in one launch:
+ *   y_i[M, N_i] = x[M, K] . dequant(W_i)^T,  i < nseg (1..4),
+ * each W_i in the same packed layout as dfmi_qmm_affine (w_q [N_i, K*bits/32],
+ * scales / biases [N_i, K/group_size], 16-byte aligned; y_i [M, N_i]).
+ *
+ * No reference counterpart as one call: it replaces the separate per-module
+ * verify_matmul launches of sibling projections that read the same input in
+ * the reference's verify forward -- q/k/v of an attention block, gate/up of
+ * an MLP (dflash_mlx/verify_linear.py:266-286, one call per
+ * VerifyQuantizedLinear) -- so that the layer pays one launch, one pipeline
+ * fill and one grid for them: the row blocks of all W_i form one streaming
+ * grid.  Shapes outside the streaming kernel (M > 32, K % 256 != 0, ...) run
+ * as nseg dfmi_qmm_affine calls on the stream, in order.  Each y_i is within
+ * fp32 summation order of what dfmi_qmm_affine returns for W_i alone (the two
+ * may split K differently); the result does not depend on scheduling.  The
+ * workspace is dfmi_qmm_multi_workspace_bytes bytes, zero-filled when
+ * created.
+ */
+typedef struct dfmi_qmm_segment {
+  const uint32_t *w_q;
+  const void *scales;
+  const void *biases;
+  void *y;
+  int64_t N;
+} dfmi_qmm_segment;
+int dfmi_qmm_affine_multi(const void *x, int x_dtype, const dfmi_qmm_segment *segs, int nseg,
+                          int64_t M, int64_t K, int group_size, int bits, void *workspace,
+                          size_t workspace_bytes, void *stream);
+size_t dfmi_qmm_multi_workspace_bytes(int64_t M, int64_t K, const int64_t *Ns, int nseg,
+                                      int group_size, int bits);
+/* Host-only plan query (no reference counterpart; for benchmarks and
+ * profiles): the kernel of the single launch dfmi_qmm_affine_multi makes,
+ * "qmm_stream_multi_kernel" (nseg >= 2) or "qmm_stream_kernel"; NULL when it
+ * makes one dfmi_qmm_affine call per matrix instead (or the shape is
+ * invalid). */
+const char *dfmi_qmm_multi_kernel_name(int64_t M, int64_t K, const int64_t *Ns, int nseg,
+                                       int group_size, int bits);
 
 /*
  * Routed-expert matmul: for each pair p < P,

@@ -77,7 +77,37 @@ def test_host_side_validation_without_gpu(lib):
                                           32, bits, None, 0, ctypes.byref(t), None) \
                 == _lib.DFMI_EINVAL
             assert b"outside the streaming kernel" in lib.dfmi_last_error()
-    for path in (3, -1):
+    # path 3 (the persistent kernel) outside its shapes
+    t3 = _lib.QmmTuning(3, 0, 0, 0)
+    assert lib.dfmi_qmm_affine_ex(None, _lib.DFMI_BF16, None, None, None, None, 24, 4096, 4096,
+                                  64, 4, None, 0, ctypes.byref(t3), None) == _lib.DFMI_EINVAL
+    assert b"outside the persistent kernel" in lib.dfmi_last_error()
+    assert lib.dfmi_qmm_kernel_name(16, 4096, 4096, 64, 8, ctypes.byref(t3)) is None
+    assert lib.dfmi_qmm_kernel_name(16, 4096, 4096, 64, 4, ctypes.byref(t3)) == b"qmm_persist_kernel"
+    # the shared-activation launch: segment count and per-segment checks
+    seg = (_lib.QmmSegment * 5)()
+    assert lib.dfmi_qmm_affine_multi(None, _lib.DFMI_BF16, seg, 5, 16, 1024, 64, 4, None, 0,
+                                     None) == _lib.DFMI_EINVAL
+    assert lib.dfmi_qmm_affine_multi(None, _lib.DFMI_BF16, seg, 0, 16, 1024, 64, 4, None, 0,
+                                     None) == _lib.DFMI_EINVAL
+    seg[0].N, seg[1].N = 64, 64
+    assert lib.dfmi_qmm_affine_multi(None, _lib.DFMI_BF16, seg, 2, 16, 1024, 64, 4, None, 0,
+                                     None) == _lib.DFMI_EINVAL
+    assert lib.dfmi_qmm_affine_multi(None, _lib.DFMI_BF16, seg, 2, 0, 1024, 64, 4, None, 0,
+                                     None) == _lib.DFMI_OK
+    # its plan: one streaming grid over the matrices' blocks, or one call per
+    # matrix outside the streaming kernel
+    ns = (ctypes.c_int64 * 3)(5120, 1024, 1024)
+    assert lib.dfmi_qmm_multi_kernel_name(16, 5120, ns, 3, 64, 4) == b"qmm_stream_multi_kernel"
+    assert lib.dfmi_qmm_multi_kernel_name(16, 5120, ns, 1, 64, 4) == b"qmm_stream_kernel"
+    assert lib.dfmi_qmm_multi_kernel_name(16, 5120, ns, 2, 64, 8) == b"qmm_stream_multi_kernel"
+    assert lib.dfmi_qmm_multi_kernel_name(40, 5120, ns, 3, 64, 4) is None      # M > 32
+    assert lib.dfmi_qmm_multi_kernel_name(16, 1088, ns, 3, 64, 4) is None      # K % 256
+    assert lib.dfmi_qmm_multi_kernel_name(16, 5120, ns, 5, 64, 4) is None
+    # the grid's split partials cover 64 columns per block of every matrix
+    ws = lib.dfmi_qmm_multi_workspace_bytes(16, 5120, ns, 3, 64, 4)
+    assert ws == 0 or (ws - 65536) % (16 * 4 * 64 * (80 + 16 + 16)) == 0
+    for path in (4, -1):
         t = _lib.QmmTuning(path, 0, 0, 0)
         assert lib.dfmi_qmm_affine_ex(None, _lib.DFMI_BF16, None, None, None, None, 16, 4096,
                                       4096, 64, 4, None, 0, ctypes.byref(t), None) \

@@ -1,0 +1,125 @@
+"""The shared-activation launch ``dfmi_qmm_affine_multi`` (q/k/v or gate/up
+of a layer in one streaming grid) against the oracle and against separate
+``dfmi_qmm_affine`` calls.
+
+Same bar as the dense tests: the reference's metric max|d| / (max|ref| +
+1e-3) <= 1e-2 plus 2 output ulps element-wise around the exact result;
+bit-exact on closed-form integer cases; each matrix's result within fp32
+summation order of its separate call."""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle
+from tests.conftest import from_dev, make_qmm_case, to_dev
+
+pytestmark = pytest.mark.gpu
+
+REL_TOL = 1e-2
+
+
+def _run(dev, x, w_q, s, b, gs, dtype="bf16", bits=4):
+    import torch
+
+    from dflash_mlx_amd import verify_qmm as vq
+
+    y = vq.quantized_matmul(to_dev(x, dtype, dev), to_dev(w_q, "u32", dev), to_dev(s, dtype, dev),
+                            to_dev(b, dtype, dev), group_size=gs, bits=bits)
+    torch.cuda.synchronize()
+    return from_dev(y, dtype)
+
+
+def _check(got, x, w_q, s, b, gs, dtype="bf16", bits=4):
+    ref = oracle.quantized_matmul(x, w_q, s, b, group_size=gs, bits=bits, dtype=dtype)
+    g = oracle.to_f32(got, dtype).astype(np.float64)
+    _, rel = oracle.parity_metrics(g, ref)
+    assert np.all(np.isfinite(g))
+    assert rel <= REL_TOL, rel
+    ulp = 2.0 ** -8 if dtype == "bf16" else 2.0 ** -11
+    assert np.all(np.abs(g - ref) <= 2 * ulp * np.abs(ref) + 1e-4 * np.abs(ref).max())
+
+
+def _kernel(M, K, Ns, bits=4):
+    from dflash_mlx_amd import _lib
+
+    ns = (ctypes.c_int64 * len(Ns))(*Ns)
+    name = _lib.load().dfmi_qmm_multi_kernel_name(M, K, ns, len(Ns), 64, bits)
+    return name.decode() if name else None
+
+
+def _multi(dev, x, mats, gs, dtype="bf16", bits=4):
+    import torch
+
+    from dflash_mlx_amd.verify_qmm import quantized_matmul_multi
+
+    ys = quantized_matmul_multi(to_dev(x, dtype, dev),
+                                [(to_dev(w, "u32", dev), to_dev(s, dtype, dev),
+                                  to_dev(b, dtype, dev)) for (w, s, b) in mats],
+                                group_size=gs, bits=bits)
+    torch.cuda.synchronize()
+    return [from_dev(y, dtype) for y in ys]
+
+
+@pytest.mark.parametrize("M,K,Ns,kernel", [
+    (16, 5120, (5120, 1024, 1024), "qmm_stream_multi_kernel"),   # 27B q/k/v (K split)
+    (16, 5120, (17408, 17408), "qmm_stream_multi_kernel"),       # 27B gate/up
+    (16, 4096, (4096, 1024, 1024), "qmm_stream_multi_kernel"),   # 9B q/k/v
+    (16, 4096, (12288, 12288), "qmm_stream_multi_kernel"),       # 9B gate/up
+    (4, 2048, (100, 3000, 64, 7), "qmm_stream_multi_kernel"),    # ragged, four matrices
+    (32, 2048, (300, 0, 700), "qmm_stream_multi_kernel"),        # two activation blocks; empty matrix
+    (16, 1024, (65,), "qmm_stream_kernel"),
+    (40, 2048, (512, 256), None),                                # M > 32: one call per matrix
+    (16, 1088, (640, 256), None)])                               # K % 256 != 0: one call per matrix
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_multi_matches_oracle_and_separate_calls(dev, M, K, Ns, kernel, dtype):
+    assert _kernel(M, K, Ns) == kernel
+    mats = []
+    x = None
+    for i, N in enumerate(Ns):
+        xx, w_q, s, b = make_qmm_case(M, K, max(N, 1), 64, dtype=dtype, seed=1000 * i + N + K)
+        x = xx if x is None else x
+        mats.append((w_q[:N], s[:N], b[:N]))
+    got = _multi(dev, x, mats, 64, dtype)
+    for (w_q, s, b), y in zip(mats, got):
+        assert y.shape == (M, w_q.shape[0])
+        if w_q.shape[0] == 0:
+            continue
+        _check(y, x, w_q, s, b, 64, dtype)
+        single = _run(dev, x, w_q, s, b, 64, dtype)
+        _, rel = oracle.parity_metrics(oracle.to_f32(y, dtype), oracle.to_f32(single, dtype))
+        assert rel <= REL_TOL
+
+
+@pytest.mark.parametrize("M,K,Ns", [(16, 4096, (4096, 1024, 1024)), (16, 2048, (3000, 100))])
+def test_multi_8bit(dev, M, K, Ns):
+    assert _kernel(M, K, Ns, bits=8) == "qmm_stream_multi_kernel"
+    mats = []
+    x = None
+    for i, N in enumerate(Ns):
+        xx, w_q, s, b = make_qmm_case(M, K, N, 64, bits=8, seed=77 + i)
+        x = xx if x is None else x
+        mats.append((w_q, s, b))
+    for (w_q, s, b), y in zip(mats, _multi(dev, x, mats, 64, bits=8)):
+        _check(y, x, w_q, s, b, 64, bits=8)
+
+
+def test_multi_closed_form_exact(dev):
+    rng = np.random.default_rng(44)
+    M, K, gs = 16, 1024, 64
+    mats = []
+    for N in (5120, 1024, 192):
+        q = rng.integers(0, 16, size=(N, K))
+        mats.append((oracle.pack(q, 4),
+                     oracle.f32_to_bf16_bits(np.full((N, K // gs), 0.125, np.float32)),
+                     oracle.f32_to_bf16_bits(np.full((N, K // gs), -1.0, np.float32))))
+    xf = np.zeros((M, K), np.float32)
+    for m in range(M):
+        xf[m, rng.choice(K, size=6, replace=False)] = rng.choice([-1.0, 1.0], size=6)
+    x = oracle.f32_to_bf16_bits(xf)
+    for (w_q, s, b), y in zip(mats, _multi(dev, x, mats, gs)):
+        want = oracle.quantized_matmul(x, w_q, s, b, group_size=gs, out_dtype="bf16")
+        assert np.array_equal(y, want)

@@ -171,3 +171,112 @@ def test_8bit_module_on_layer_shapes(dev, monkeypatch, K, N):
     y = verify(x)
     assert torch.equal(y, _direct(ql, x))
     _oracle_check(ql, x, y)
+
+
+def _layer(dev, K, Nq, Nkv, Ni, seed, bias=False):
+    import torch
+
+    class Attn(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.q_proj = _mk_ql(dev, K, Nq, seed=seed, std=0.02, bias=bias)
+            self.k_proj = _mk_ql(dev, K, Nkv, seed=seed + 1, std=0.02, bias=bias)
+            self.v_proj = _mk_ql(dev, K, Nkv, seed=seed + 2, std=0.02, bias=bias)
+
+    class MLP(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.gate_proj = _mk_ql(dev, K, Ni, seed=seed + 3, std=0.02)
+            self.up_proj = _mk_ql(dev, K, Ni, seed=seed + 4, std=0.02)
+
+    class Layer(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.self_attn = Attn()
+            self.mlp = MLP()
+
+    return Layer()
+
+
+@pytest.mark.parametrize("M", [16, 4])
+@pytest.mark.parametrize("bias", [False, True])
+def test_fused_siblings(dev, monkeypatch, M, bias):
+    """install_verify_linears(fuse_siblings=True): q/k/v and gate/up each run
+    as one shared-activation launch in the model's own call order; every
+    member's output equals quantized_matmul_multi's for it (+ bias) bit for
+    bit, whatever order the members are called in, and is within 1e-2 of the
+    unfused module."""
+    import torch
+
+    from dflash_mlx_amd.verify_linear import install_verify_linears
+    from dflash_mlx_amd.verify_qmm import quantized_matmul_multi
+
+    monkeypatch.setenv("DFLASH_VERIFY_QMM", "1")
+    K = 2048
+    fused = _layer(dev, K, 2048, 512, 4096, seed=11, bias=bias)
+    plain = _layer(dev, K, 2048, 512, 4096, seed=11, bias=bias)
+    assert install_verify_linears(fused, fuse_siblings=True) == 5
+    assert install_verify_linears(plain) == 5
+    x = _x(dev, M, K, seed=12, scale=1.0)
+    for parent, names in ((fused.self_attn, ("q_proj", "k_proj", "v_proj")),
+                          (fused.mlp, ("gate_proj", "up_proj"))):
+        mods = [getattr(parent, n) for n in names]
+        direct = quantized_matmul_multi(x, [(m.weight, m.scales, m.biases) for m in mods],
+                                        group_size=64, bits=4)
+        want = [d + m.bias if m.has_bias() else d for d, m in zip(direct, mods)]
+        for order in (range(len(mods)), reversed(range(len(mods)))):
+            got = {i: mods[i](x) for i in order}
+            for i in range(len(mods)):
+                assert torch.equal(got[i], want[i])
+        ref_parent = plain.self_attn if parent is fused.self_attn else plain.mlp
+        for n, w in zip(names, want):
+            ref = getattr(ref_parent, n)(x).float()
+            rel = float((w.float() - ref).abs().max() / (ref.abs().max() + 1e-3))
+            assert rel <= REL_TOL
+    # a member called with another input recomputes its group for that input
+    x2 = _x(dev, M, K, seed=13, scale=1.0)
+    q1 = fused.self_attn.q_proj(x)
+    k2 = fused.self_attn.k_proj(x2)
+    direct2 = quantized_matmul_multi(
+        x2, [(m.weight, m.scales, m.biases) for m in
+             (fused.self_attn.q_proj, fused.self_attn.k_proj, fused.self_attn.v_proj)],
+        group_size=64, bits=4)
+    kb = fused.self_attn.k_proj.bias
+    assert torch.equal(k2, direct2[1] + kb if kb is not None else direct2[1])
+    assert q1.shape == (M, 2048)
+
+
+def test_fused_siblings_graph_replay(dev, monkeypatch):
+    """The grouped calls captured in a HIP graph replay to the eager result
+    (replays interleaved with eager work and synchronisations)."""
+    import torch
+
+    from dflash_mlx_amd.verify_linear import install_verify_linears, prewarm_verify_kernels
+
+    monkeypatch.setenv("DFLASH_VERIFY_QMM", "1")
+    K = 2048
+    model = _layer(dev, K, 2048, 512, 4096, seed=21)
+    install_verify_linears(model, fuse_siblings=True)
+    prewarm_verify_kernels(model)
+    x = _x(dev, 16, K, seed=22, scale=1.0)
+
+    def fwd():
+        a = model.self_attn
+        return (a.q_proj(x), a.k_proj(x), a.v_proj(x), model.mlp.gate_proj(x),
+                model.mlp.up_proj(x))
+
+    eager = [t.clone() for t in fwd()]
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        fwd()
+    stream.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        outs = fwd()
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        for o, e in zip(outs, eager):
+            assert torch.equal(o, e)
+        fwd()  # eager work between replays
+        torch.cuda.synchronize()
