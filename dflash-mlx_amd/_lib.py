@@ -56,6 +56,9 @@ _SIGNATURES = {
                                                ctypes.POINTER(QmmTuning)]),
     "dfmi_qmm_workspace_bytes_ex": (_size, [_i64, _i64, _i64, _int, _int,
                                             ctypes.POINTER(QmmTuning)]),
+    "dfmi_qmm_affine_noalloc": (_int, [_c_void_p, _int, _c_void_p, _c_void_p, _c_void_p,
+                                       _c_void_p, _i64, _i64, _i64, _int, _int, _c_void_p]),
+    "dfmi_qmm_noalloc_scratch_bytes": (_size, []),
     "dfmi_qmm_affine_multi": (_int, [_c_void_p, _int, ctypes.POINTER(QmmSegment), _int, _i64,
                                      _i64, _int, _int, _c_void_p, _size, _c_void_p]),
     "dfmi_qmm_multi_workspace_bytes": (_size, [_i64, _i64, ctypes.POINTER(ctypes.c_int64), _int,

@@ -9,6 +9,7 @@
 // from L2 by every workgroup: x bytes / weight bytes = 57 / (16*NT)).
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 
 #include "dfmi_core.h"
 #include "dfmi_host.h"
@@ -701,6 +702,82 @@ extern "C" int dfmi_qmm_affine(const void* x, int x_dtype, const uint32_t* w_q, 
                                void* stream) {
   return dfmi_qmm_affine_ex(x, x_dtype, w_q, scales, biases, y, M, K, N, group_size, bits,
                             workspace, workspace_bytes, nullptr, stream);
+}
+
+// ---------------------------------------------------------------------------
+// dfmi_qmm_affine_noalloc: dfmi_qmm_affine with its split-K workspace (block
+// counters, then fp32 partials) in this static device array instead of a
+// caller's buffer, for callers that cannot allocate device memory.  Each GPU
+// the library runs on holds one copy until the process ends.  In host code
+// `scratch` names a host-side stand-in; the device address of each GPU's copy
+// comes from hipGetSymbolAddress, once per device, and only that address is
+// passed to kernels.
+constexpr size_t kScratchBytes = kCounterBytes + ((size_t)8 << 20);
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace dfmi {
+
+constexpr int kScratchDevices = 64;
+
+__global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* p, int n) {
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) p[i] = 0u;
+}
+
+// This device's copy of `scratch`; on its first call per device the counter
+// region is cleared by a kernel on `st` (ahead of the caller's launch in
+// stream order; a kernel node, so graph capture may record it).
+static int scratch_of_device(hipStream_t st, void** out) {
+  static std::mutex mu;
+  static void* ptrs[kScratchDevices] = {};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kScratchDevices) {
+    set_error("dfmi_qmm_affine_noalloc: no usable current device (%s, device %d)",
+              hipGetErrorString(e), dev);
+    return DFMI_ELAUNCH;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ptrs[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      set_error("dfmi_qmm_affine_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s",
+                dev, hipGetErrorString(e));
+      return DFMI_ELAUNCH;
+    }
+    hipLaunchKernelGGL(zero_words_kernel, dim3(64), dim3(256), 0, st, static_cast<uint32_t*>(p),
+                       (int)(kCounterBytes / 4));
+    const int rc = check_launch("dfmi_qmm_affine_noalloc (scratch clear)");
+    if (rc != DFMI_OK) return rc;
+    ptrs[dev] = p;
+  }
+  *out = ptrs[dev];
+  return DFMI_OK;
+}
+
+}  // namespace dfmi
+
+extern "C" size_t dfmi_qmm_noalloc_scratch_bytes(void) { return kScratchBytes; }
+
+extern "C" int dfmi_qmm_affine_noalloc(const void* x, int x_dtype, const uint32_t* w_q,
+                                       const void* scales, const void* biases, void* y, int64_t M,
+                                       int64_t K, int64_t N, int group_size, int bits,
+                                       void* stream) {
+  int rc = validate_qmm(x_dtype, M, K, N, group_size, bits);
+  if (rc != DFMI_OK) return rc;
+  if (M == 0 || N == 0) return DFMI_OK;
+  const size_t need = dfmi_qmm_workspace_bytes_ex(M, K, N, group_size, bits, nullptr);
+  if (need > kScratchBytes) {
+    set_error("dfmi_qmm_affine_noalloc: shape M=%lld K=%lld N=%lld needs %zu workspace bytes, "
+              "above the %zu-byte static scratch (use dfmi_qmm_affine with a workspace)",
+              (long long)M, (long long)K, (long long)N, need, kScratchBytes);
+    return DFMI_ENOSPC;
+  }
+  void* ws = nullptr;
+  rc = scratch_of_device(static_cast<hipStream_t>(stream), &ws);
+  if (rc != DFMI_OK) return rc;
+  return dfmi_qmm_affine_ex(x, x_dtype, w_q, scales, biases, y, M, K, N, group_size, bits, ws,
+                            kScratchBytes, nullptr, stream);
 }
 
 extern "C" size_t dfmi_qmm_multi_workspace_bytes(int64_t M, int64_t K, const int64_t* Ns,

@@ -111,6 +111,25 @@ size_t dfmi_qmm_workspace_bytes_ex(int64_t M, int64_t K, int64_t N, int group_si
                                    const dfmi_qmm_tuning *tuning);
 
 /*
+ * dfmi_qmm_affine that allocates nothing and takes no workspace.  No
+ * counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  The split-K workspace (block counters, then fp32
+ * partials) lives in a static device array of dfmi_qmm_noalloc_scratch_bytes()
+ * bytes (64 KiB + 8 MiB) that every GPU the library runs on holds until the
+ * process ends.  The automatic plan of the shape must fit it, else
+ * DFMI_ENOSPC (nothing launched); the same plan and kernels as
+ * dfmi_qmm_affine, so the result is bit-identical to it.  The first call on a
+ * device clears the array's counters with a kernel on `stream`.  All calls on
+ * one GPU share the array: calls that overlap in time on one GPU (different
+ * streams, or host threads) race on it and must be serialised by the caller.
+ */
+int dfmi_qmm_affine_noalloc(const void *x, int x_dtype, const uint32_t *w_q, const void *scales,
+                            const void *biases, void *y, int64_t M, int64_t K, int64_t N,
+                            int group_size, int bits, void *stream);
+size_t dfmi_qmm_noalloc_scratch_bytes(void);
+
+/*
  * Several matmuls that share their activations, in one launch:
  *   y_i[M, N_i] = x[M, K] . dequant(W_i)^T,  i < nseg (1..4),
  * each W_i in the same packed layout as dfmi_qmm_affine (w_q [N_i, K*bits/32],
