@@ -141,7 +141,11 @@ static void launch_tag(int gs, const DensePlan& p, hipStream_t st, const DenseAr
 // no plain store is published across workgroups.
 
 constexpr size_t kCounterBytes = 65536;
-// plain calls route to the persistent kernel automatically
+// The persistent wide kernel (dfmi_persist.hip) as the automatic choice for
+// plain and shared-activation calls: off.  On MI355X it measured slower than
+// the streaming grid on every M = 16 verify shape (27B q/k/v fused 18.8 vs
+// 12.0 us, gate/up fused 40.9 vs 33.4 us, 151936 x 5120 137 vs 106 us), so it
+// runs only when tuning path 3 asks for it.
 constexpr bool kPersistAuto = false;
 constexpr int kMaxCounters = (int)(kCounterBytes / 4);
 constexpr int kMaxSeg = 4;  // weight matrices of one shared-activation launch
@@ -534,10 +538,9 @@ static bool valid_path(const dfmi_qmm_tuning* tune) {
   return !tune || (tune->path >= 0 && tune->path <= 3);
 }
 
-// The persistent streaming kernel takes a plain call when the automatic
-// choice (or path 3) asks for it and its planner accepts the shape.  The
-// automatic choice uses it for every shape it takes (it measured faster than
-// the per-call streaming grid on every M = 16 verify shape).
+// The persistent streaming kernel takes a plain call when path 3 (or the
+// automatic choice, with kPersistAuto) asks for it and its planner accepts the
+// shape.
 static bool use_persist(int64_t M, int64_t K, int64_t N, int gs, int bits,
                         const dfmi_qmm_tuning* tune, size_t* ws) {
   const int path = tune ? tune->path : 0;
@@ -786,6 +789,8 @@ extern "C" size_t dfmi_qmm_multi_workspace_bytes(int64_t M, int64_t K, const int
   for (int i = 0; i < nseg; ++i)
     if (validate_qmm(DFMI_BF16, M, K, Ns[i], group_size, bits) != DFMI_OK) return 0;
   if (M == 0) return 0;
+  size_t pws = 0;
+  if (kPersistAuto && dfmi_persist_plan(M, K, Ns, nseg, group_size, bits, &pws)) return pws;
   const int64_t cols = multi_stream_cols(M, K, Ns, nseg, group_size, bits);
   if (cols > 0) {
     StreamPlan p;
@@ -802,6 +807,8 @@ extern "C" const char* dfmi_qmm_multi_kernel_name(int64_t M, int64_t K, const in
   if (!Ns || nseg < 1 || nseg > kMaxSeg) return nullptr;
   for (int i = 0; i < nseg; ++i)
     if (validate_qmm(DFMI_BF16, M, K, Ns[i], group_size, bits) != DFMI_OK) return nullptr;
+  if (kPersistAuto && dfmi_persist_plan(M, K, Ns, nseg, group_size, bits, nullptr))
+    return "qmm_persist_kernel";
   if (multi_stream_cols(M, K, Ns, nseg, group_size, bits) <= 0) return nullptr;
   return nseg == 1 ? "qmm_stream_kernel" : "qmm_stream_multi_kernel";
 }
@@ -835,6 +842,9 @@ extern "C" int dfmi_qmm_affine_multi(const void* x, int x_dtype, const dfmi_qmm_
       return DFMI_EINVAL;
     }
   }
+  if (kPersistAuto && dfmi_persist_plan(M, K, Ns, nseg, group_size, bits, nullptr))
+    return dfmi_persist_launch(x, x_dtype, segs, nseg, M, K, group_size, workspace,
+                               workspace_bytes, stream);
   const int64_t cols = multi_stream_cols(M, K, Ns, nseg, group_size, bits);
   if (cols > 0) {
     StreamSegs m{};

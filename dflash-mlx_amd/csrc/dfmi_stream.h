@@ -116,11 +116,17 @@ __device__ inline uint32_t opaque(uint32_t v) {
   return v;
 }
 
-template <typename Tag, int GS, int MT, int WV, int SBPC = kSbPieces, int BITS = 4>
+// RW row groups: the workgroup's WV wavefronts are RW groups of KW = WV / RW;
+// group r owns rows 64 r .. 64 r + 63 of the block (NB = 64 RW rows), and
+// wavefront k of a group takes the k-th 64-k slice of every step (CK = 64 KW
+// k).  All groups read the same activation stage, so two groups halve the
+// activation bytes per weight byte.
+template <typename Tag, int GS, int MT, int WV, int SBPC = kSbPieces, int BITS = 4, int RW = 1>
 struct Stream {
-  static constexpr int NT = kStreamTiles;
-  static constexpr int NB = kStreamRows;
-  static constexpr int CK = 64 * WV;        // k per step
+  static constexpr int NT = kStreamTiles;   // 16-row tiles per wavefront
+  static constexpr int KW = WV / RW;        // wavefronts along k
+  static constexpr int NB = kStreamRows * RW;
+  static constexpr int CK = 64 * KW;        // k per step
   static constexpr int GPC = CK / GS;       // quantisation groups per step
   static constexpr int XROW = CK * 2;       // bytes of one activation row per step
   static constexpr int XPPR = CK / 8;       // 16-byte pieces per activation row
@@ -132,6 +138,7 @@ struct Stream {
   static constexpr int SWZ = WPPR < 16 ? WPPR : 16;
   static_assert(WV == 4 || WV == 8, "wavefronts");
   static_assert(BITS == 4 || BITS == 8, "weight bits");
+  static_assert(RW == 1 || (RW == 2 && WV == 8 && MT == 1 && BITS == 4), "row groups");
   // 8-bit values are dequantised exactly: bf16 by conversion (no offset),
   // f16 by the 1024 magic
   static constexpr float OFFQ =
@@ -146,8 +153,9 @@ struct Stream {
   // weights with one activation block and 4 wavefronts likewise fit 80 KB in
   // two stages; with two blocks they would still need 96 KB (one workgroup
   // per CU), so they keep three.
+  // Two row groups (one workgroup per CU) take four stages.
   static constexpr int DEPTH =
-      (MT == 2 && BITS == 4) || (MT == 1 && BITS == 8 && WV == 4) ? 2 : 3;
+      RW == 2 ? 4 : ((MT == 2 && BITS == 4) || (MT == 1 && BITS == 8 && WV == 4) ? 2 : 3);
   // gs >= 64: a lane's two k-blocks take adjacent words (one 8-byte LDS read);
   // gs = 32: k-block j is group 2*wave + j, so the blocks stay group-pure.
   static constexpr bool PAIR = GS >= 64;
@@ -226,9 +234,10 @@ struct Stream {
     uint32_t bv[NT];    // dword holding this lane's bias(es)
   };
 
-  // word (= 8-k piece) of the step that lane group kg feeds k-block j with
-  __device__ static inline int piece_of(int wave, int kg, int j) {
-    return PAIR ? 8 * wave + 2 * kg + j : 8 * wave + 4 * j + kg;
+  // word (= 8-k piece) of the step that lane group kg of the wavefront with
+  // k index kw feeds k-block j with
+  __device__ static inline int piece_of(int kw, int kg, int j) {
+    return PAIR ? 8 * kw + 2 * kg + j : 8 * kw + 4 * j + kg;
   }
 
   __device__ static inline Lane lane_setup(const Ctx& cx) {
@@ -260,17 +269,20 @@ struct Stream {
       const int n = min(cx.n0 + (r >= cx.split ? r - cx.split : r), cx.N - 1);
       L.wg[i] = (uint32_t)n * (uint32_t)(cx.K / 8 * BITS) + (uint32_t)piece * 16u;
     }
-    // fragment reads (row m = col of M-block 0, row r = col of tile 0; the
-    // other blocks / tiles are whole-row multiples away)
+    // fragment reads (row m = col of M-block 0, row r = col of tile 0 of the
+    // wavefront's row group; the other blocks / tiles are whole-row multiples
+    // away; SWZ and SBPC divide 64, so the group's rows keep the keys of col)
+    const int kw = cx.wave % KW, rg = cx.wave / KW;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      L.xo[j] = (uint32_t)(col * XROW + ((piece_of(cx.wave, kg, j) ^ col) * 16));
-      const int byte = piece_of(cx.wave, kg, j) * 4 * WPK;
-      L.wo[j] = (uint32_t)(col * WROW + (((byte >> 4) ^ (col % SWZ)) * 16) + (byte & 15));
+      L.xo[j] = (uint32_t)(col * XROW + ((piece_of(kw, kg, j) ^ col) * 16));
+      const int byte = piece_of(kw, kg, j) * 4 * WPK;
+      L.wo[j] = (uint32_t)((64 * rg + col) * WROW + (((byte >> 4) ^ (col % SWZ)) * 16) +
+                           (byte & 15));
     }
-    L.sbr = (uint32_t)(col * SBP);
+    L.sbr = (uint32_t)((64 * rg + col) * SBP);
     L.swz = (uint32_t)(col % SBPC);
-    const int half = PAIR ? (((cx.wave * 64) / GS) & 1) : 0;
+    const int half = PAIR ? (((kw * 64) / GS) & 1) : 0;
     L.hsel = half ? 0x03020c0cu : 0x01000c0cu;
     return L;
   }
@@ -340,8 +352,8 @@ struct Stream {
     const char* ws1 = dfmi_smem + (L.wo[1] + wb);
     // this step's group in the window: piece gr / 8 (stored at slot
     // (gr / 8) ^ (col % SBPC)), dword (gr % 8) / 2 of the piece
-    const uint32_t gr =
-        (uint32_t)(c * GPC + (PAIR ? (cx.wave * 64) / GS : 2 * cx.wave) - g0w);
+    const int kw = cx.wave % KW;
+    const uint32_t gr = (uint32_t)(c * GPC + (PAIR ? (kw * 64) / GS : 2 * kw) - g0w);
     const char* sbp = dfmi_smem + SB_OFF + cx.sb_base +
                       (L.sbr + (((gr >> 3) ^ L.swz) << 4) + ((gr & 7) >> 1) * 4);
 #pragma unroll

@@ -51,9 +51,9 @@ const char *dfmi_last_error(void);
  *   path: 1 = general kernel, 2 = streaming kernel (DFMI_EINVAL if the shape
  *         is outside it: M <= 32, K % 256 == 0, K % (8*group_size) == 0;
  *         checked for both weight widths), 3 = persistent stream-K kernel
- *         (DFMI_EINVAL outside M <= 16, int4, K % 256 == 0, K >= 512, K a
- *         multiple of 8 groups, and its planner); any other value is
- *         DFMI_EINVAL;
+ *         with 128-row blocks, one workgroup per CU (DFMI_EINVAL outside
+ *         M <= 16, int4, K % 256 == 0, K a multiple of 8 groups, at most
+ *         16384 blocks); any other value is DFMI_EINVAL;
  *   tiles_per_wave: general kernel, 16-row weight tiles per wavefront (1, 2,
  *         4); the streaming kernel always covers 64 rows per workgroup;
  *   waves_per_block: general kernel, wavefronts of a workgroup that split K

@@ -56,13 +56,13 @@ def _kernel(M, K, N, gs=64, path=3):
 
 
 @pytest.mark.parametrize("M,K,N", [
-    (16, 5120, 5120),    # 80 blocks over 512 workgroups: 3-4 workgroups per block
-    (16, 5120, 1024),    # 16 blocks: 2-step ranges, 10 parts per block
-    (16, 5120, 17408),   # 272 blocks: ranges of 10-11 steps across block ends
-    (16, 17408, 5120),   # K beyond one scale window: every range a part
-    (16, 4096, 12288),   # 192 blocks
-    (16, 5120, 34816),   # 544 blocks: a whole block plus parts per range (fused gate/up size)
-    (16, 12288, 4096)])
+    (16, 5120, 5120),    # 40 blocks of 128 rows, 5 per XCD: ranges of 3-4 steps
+    (16, 5120, 1024),    # 8 blocks, one per XCD: 20 one-step parts per block
+    (16, 5120, 17408),   # 136 blocks: ranges of 10-11 steps across block ends
+    (16, 17408, 5120),   # 68 steps per block: several window segments per range
+    (16, 4096, 12288),   # 96 blocks
+    (16, 5120, 34816),   # 272 blocks, 34 per XCD (fused gate/up size)
+    (16, 12288, 4096)])  # 32 blocks, 48 steps
 def test_persist_layer_shapes(dev, M, K, N):
     assert _kernel(M, K, N) == "qmm_persist_kernel"
     x, w_q, s, b = make_qmm_case(M, K, N, 64, seed=K + N + 7)
@@ -74,7 +74,7 @@ def test_persist_layer_shapes(dev, M, K, N):
 @pytest.mark.parametrize("dtype", ["bf16", "f16"])
 def test_persist_m_gs_dtype(dev, M, gs, dtype):
     # 2048 x 3000: ragged N (the last block's rows past N are clamped loads,
-    # never stored), 47 blocks x 8 steps over 188 workgroups
+    # never stored), 24 blocks x 8 steps: one-step parts, 8 per block
     K, N = 2048, 3000
     x, w_q, s, b = make_qmm_case(M, K, N, gs, dtype=dtype, seed=M * 10 + gs)
     _check(_run(dev, x, w_q, s, b, gs, dtype), x, w_q, s, b, gs, dtype)
@@ -82,8 +82,8 @@ def test_persist_m_gs_dtype(dev, M, gs, dtype):
 
 @pytest.mark.parametrize("K,N", [(1024, 70000), (2048, 20000), (1024, 13)])
 def test_persist_many_units_and_tiny(dev, K, N):
-    # 1094 and 313 blocks (several whole blocks per range, four-step blocks
-    # at K = 1024), and a single ragged block
+    # 547 and 157 blocks (several whole blocks per range, four-step blocks
+    # at K = 1024), and a single ragged block on one XCD (four one-step parts)
     x, w_q, s, b = make_qmm_case(16, K, N, 64, seed=K + N)
     _check(_run(dev, x, w_q, s, b, 64), x, w_q, s, b, 64)
 
@@ -119,4 +119,10 @@ def test_persist_deterministic(dev):
 def test_persist_rejects_outside_shapes(dev):
     assert _kernel(24, 2048, 256) is None      # M > 16
     assert _kernel(16, 1088, 256) is None      # K not a multiple of 256
-    assert _kernel(16, 256, 256) is None       # a single 256-k step
+
+
+def test_persist_single_step(dev):
+    # K = 256 (group 32, so K holds whole 8-group pieces): one step per
+    # block, every range one position
+    x, w_q, s, b = make_qmm_case(16, 256, 3000, 32, seed=9)
+    _check(_run(dev, x, w_q, s, b, 32), x, w_q, s, b, 32)
