@@ -6,7 +6,9 @@
  * null stream).  All launches are stream-ordered and asynchronous; a return of
  * DFMI_OK means the work was enqueued.  No function allocates or frees device
  * memory and none keeps a pointer past its return.  Functions are reentrant;
- * the only process state is the thread-local error string.
+ * the process state is the thread-local error string and, for
+ * dfmi_qmm_affine_noalloc only, its static device scratch array and the
+ * per-device address of it (set once, under a lock).
  *
  * Packed-weight layout (the bytes dflash-mlx and MLX hand to the kernels,
  * dflash_mlx/verify_qmm.py:97-115): w_q uint32 [N, K*bits/32] row-major,
