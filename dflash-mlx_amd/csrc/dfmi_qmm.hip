@@ -160,6 +160,7 @@ struct StreamArgs {
   int n_blocks;
   int xcd_map;
   int pstride;  // columns of a partial row: N (one matrix) or 64 x n_blocks
+  int whole;    // blocks [0, whole) run unsplit, one workgroup each; the rest kp-way split
 };
 
 // One weight matrix of a launch: the launch's blocks blk0 .. blk0 +
@@ -179,8 +180,19 @@ struct StreamSegs {
   int nseg;
 };
 
-// workgroup L -> (block nb, K split kpi)
-__device__ inline void stream_unit_of(int L, int kp, int xcd_map, int& nb, int& kpi) {
+// workgroup L -> (block nb, K split kpi of kpw).  Workgroups [0, whole) take
+// blocks [0, whole) whole; the rest take the kp splits of the later blocks
+// (whole is a multiple of 8, so L - whole keeps L's XCD).
+__device__ inline void stream_unit_of(int L, int whole, int kp, int xcd_map, int& nb, int& kpi,
+                                      int& kpw) {
+  if (L < whole) {
+    nb = L;
+    kpi = 0;
+    kpw = 1;
+    return;
+  }
+  L -= whole;
+  kpw = kp;
   if (xcd_map) {
     // consecutive workgroup ids go to different XCDs (id & 7): give the kp
     // splits of one block to one XCD so the block's partials and counter
@@ -193,12 +205,13 @@ __device__ inline void stream_unit_of(int L, int kp, int xcd_map, int& nb, int& 
     nb = L / kp;
     kpi = L - nb * kp;
   }
+  nb += whole;
 }
 
-// Block nb (of matrix g), K split kpi.
+// Block nb (of matrix g), K split kpi of kp.
 template <typename Tag, int GS, int MT, int WV, int BITS, int SBPC>
 __device__ __forceinline__ void qmm_stream_body(const StreamArgs& a, const StreamSeg& g, int nb,
-                                                int kpi) {
+                                                int kpi, int kp) {
   using S = Stream<Tag, GS, MT, WV, SBPC, BITS>;
   constexpr int kThreads = 64 * WV;
   typename S::Ctx cx;
@@ -214,8 +227,8 @@ __device__ __forceinline__ void qmm_stream_body(const StreamArgs& a, const Strea
   cx.lane = threadIdx.x & 63;
   cx.wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   cx.dense();
-  const int c0 = (int)((int64_t)kpi * a.chunks / a.kp);
-  const int c1 = (int)((int64_t)(kpi + 1) * a.chunks / a.kp);
+  const int c0 = (int)((int64_t)kpi * a.chunks / kp);
+  const int c1 = (int)((int64_t)(kpi + 1) * a.chunks / kp);
   f32x4 acc[S::NT][MT];
 #pragma unroll
   for (int t = 0; t < S::NT; ++t)
@@ -251,7 +264,7 @@ __device__ __forceinline__ void qmm_stream_body(const StreamArgs& a, const Strea
     ni[q] = cx.n0 + (tm / MT) * 16 + (l & 15);
     mi[q] = (tm % MT) * 16 + 4 * (l >> 4) + j;
   }
-  if (a.kp == 1) {
+  if (kp == 1) {
 #pragma unroll
     for (int q = 0; q < PER; ++q)
       if (mi[q] < a.M && ni[q] < g.N) g.y[(int64_t)mi[q] * g.N + ni[q]] = Num<Tag>::f2h(v[q]);
@@ -269,7 +282,7 @@ __device__ __forceinline__ void qmm_stream_body(const StreamArgs& a, const Strea
   if (threadIdx.x == 0) {
     const unsigned prev =
         __hip_atomic_fetch_add(&a.counters[nb], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    *s_last = (prev == (unsigned)(a.kp - 1)) ? 1 : 0;
+    *s_last = (prev == (unsigned)(kp - 1)) ? 1 : 0;
   }
   stage_barrier<0>();
   if (!*s_last) return;
@@ -286,13 +299,13 @@ __device__ __forceinline__ void qmm_stream_body(const StreamArgs& a, const Strea
     off[q] = ok[q] ? (int64_t)mi[q] * a.pstride + (int64_t)g.blk0 * S::NB + ni[q] : 0;
   }
   const int64_t split = (int64_t)a.M * a.pstride;
-  for (int q0 = 0; q0 < a.kp; q0 += 4) {
+  for (int q0 = 0; q0 < kp; q0 += 4) {
     // unconditional loads (a split past kp re-reads the last one and is
     // dropped), so the block is straight-line code with one wait
     float t[4][PER];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int64_t base = (int64_t)min(q0 + j, a.kp - 1) * split;
+      const int64_t base = (int64_t)min(q0 + j, kp - 1) * split;
 #pragma unroll
       for (int q = 0; q < PER; ++q)
         t[j][q] = __hip_atomic_load(a.partials + base + off[q], __ATOMIC_RELAXED,
@@ -301,7 +314,7 @@ __device__ __forceinline__ void qmm_stream_body(const StreamArgs& a, const Strea
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int q = 0; q < PER; ++q) sum[q] += (q0 + j < a.kp) ? t[j][q] : 0.f;
+      for (int q = 0; q < PER; ++q) sum[q] += (q0 + j < kp) ? t[j][q] : 0.f;
   }
 #pragma unroll
   for (int q = 0; q < PER; ++q)
@@ -312,6 +325,7 @@ __device__ __forceinline__ void qmm_stream_body(const StreamArgs& a, const Strea
 
 struct StreamPlan {
   int MT, WV, kp, chunks, n_blocks, grid_x, xcd_map, lds;
+  int whole;  // blocks run unsplit ahead of the kp-way split ones
   int bits;  // 4 or 8
   int sbpc;  // scale / bias window pieces (8-bit with 8 wavefronts: 8, to fit LDS)
   size_t ws_bytes;
@@ -370,8 +384,27 @@ static int plan_stream(int64_t M, int64_t K, int64_t N, int gs, int bits,
   p.sbpc = stream_sb_pieces(bits, p.WV);
   const int max_chunks = sb_max_groups(p.sbpc) / (64 * p.WV / gs);
   p.kp = std::max(p.kp, (p.chunks + max_chunks - 1) / max_chunks);
+  p.whole = 0;
   p.xcd_map = (p.n_blocks % 8 == 0) ? 1 : 0;
-  p.grid_x = p.n_blocks * p.kp;
+  // A grid a little past whole rounds of the workgroups that run at once
+  // (two per CU with 4 wavefronts, one with 8) would end with a round of a
+  // few whole blocks, as long as a full round: a workgroup streams at a
+  // latency-bound rate whatever the others do (27B-class gate/up, 544 blocks
+  // on 512 slots: 32.8 us, 512 blocks: 24.9 us).  So the whole rounds run
+  // unsplit and the leftover blocks (at most a quarter round) are split
+  // finely enough to spread over every slot.
+  const int slots = p.WV == 8 ? 256 : 512;
+  if (!(tune && tune->k_splits > 0) && p.kp == 1 && p.n_blocks > slots &&
+      p.n_blocks <= kMaxCounters) {
+    const int whole = (p.n_blocks / slots) * slots;
+    const int left = p.n_blocks - whole;
+    if (left > 0 && 4 * left <= slots) {
+      p.whole = whole;
+      p.kp = std::max(1, std::min((int)std::lround((double)slots / left), p.chunks));
+      p.xcd_map = (left % 8 == 0) ? 1 : 0;
+    }
+  }
+  p.grid_x = p.whole + (p.n_blocks - p.whole) * p.kp;
   p.ws_bytes = p.kp > 1 ? kCounterBytes + (size_t)p.kp * (size_t)M * (size_t)N * 4u : 0;
   return DFMI_OK;
 }
@@ -382,28 +415,28 @@ template <typename Tag, int GS, int MT, int WV, int BITS, int SBPC>
 __global__ __launch_bounds__(64 * WV) void qmm_stream_kernel(
     const uint16_t* x, const uint32_t* w, const uint16_t* s, const uint16_t* b, uint16_t* y,
     float* partials, uint32_t* counters, int M, int K, int N, int chunks, int kp, int n_blocks,
-    int xcd_map) {
-  int nb, kpi;
-  stream_unit_of(blockIdx.x, kp, xcd_map, nb, kpi);
+    int xcd_map, int whole) {
+  int nb, kpi, kpw;
+  stream_unit_of(blockIdx.x, whole, kp, xcd_map, nb, kpi, kpw);
   if (nb >= n_blocks) return;  // uniform, before any barrier
   qmm_stream_body<Tag, GS, MT, WV, BITS, SBPC>(
-      StreamArgs{x, partials, counters, M, K, chunks, kp, n_blocks, xcd_map, N},
-      StreamSeg{w, s, b, y, N, 0}, nb, kpi);
+      StreamArgs{x, partials, counters, M, K, chunks, kp, n_blocks, xcd_map, N, whole},
+      StreamSeg{w, s, b, y, N, 0}, nb, kpi, kpw);
 }
 
 // Several weight matrices over the same activations (q / k / v, gate / up):
 // their row blocks form one grid.
 template <typename Tag, int GS, int MT, int WV, int BITS, int SBPC>
 __global__ __launch_bounds__(64 * WV) void qmm_stream_multi_kernel(StreamArgs a, StreamSegs m) {
-  int nb, kpi;
-  stream_unit_of(blockIdx.x, a.kp, a.xcd_map, nb, kpi);
+  int nb, kpi, kpw;
+  stream_unit_of(blockIdx.x, a.whole, a.kp, a.xcd_map, nb, kpi, kpw);
   if (nb >= a.n_blocks) return;  // uniform, before any barrier
   // the matrix holding block nb (constant indices: the table stays in SGPRs)
   StreamSeg g = m.seg[0];
 #pragma unroll
   for (int i = 1; i < kMaxSeg; ++i)
     if (i < m.nseg && nb >= m.seg[i].blk0) g = m.seg[i];
-  qmm_stream_body<Tag, GS, MT, WV, BITS, SBPC>(a, g, nb, kpi);
+  qmm_stream_body<Tag, GS, MT, WV, BITS, SBPC>(a, g, nb, kpi, kpw);
 }
 
 template <typename Tag, int GS, int MT, int WV, int BITS>
@@ -415,7 +448,7 @@ static void launch_stream_t(const StreamPlan& p, hipStream_t st, const StreamArg
     const StreamSeg& g = m.seg[0];
     hipLaunchKernelGGL((qmm_stream_kernel<Tag, GS, MT, WV, BITS, SBPC>), dim3(p.grid_x),
                        dim3(64 * WV), lds, st, a.x, g.w, g.s, g.b, g.y, a.partials, a.counters,
-                       a.M, a.K, g.N, a.chunks, a.kp, a.n_blocks, a.xcd_map);
+                       a.M, a.K, g.N, a.chunks, a.kp, a.n_blocks, a.xcd_map, a.whole);
   } else {
     hipLaunchKernelGGL((qmm_stream_multi_kernel<Tag, GS, MT, WV, BITS, SBPC>), dim3(p.grid_x),
                        dim3(64 * WV), lds, st, a, m);
@@ -579,6 +612,7 @@ static int launch_streaming(const void* x, int x_dtype, const StreamSegs& m, int
   a.n_blocks = p.n_blocks;
   a.xcd_map = p.xcd_map;
   a.pstride = (int)n_cols;
+  a.whole = p.whole;
   allow_lds_all();
   if (x_dtype == DFMI_BF16) launch_stream<BF16>(gs, p, st, a, m);
   else launch_stream<F16>(gs, p, st, a, m);

@@ -169,3 +169,15 @@ def test_streaming_split_plans(lib):
     # 8-bit, M = 16: the unsplit 192-block grid runs as 4 wavefronts, 2 splits
     assert splits(16, 4096, 12288, 8) == 2
     assert splits(16, 4096, 4096, 8) == 4
+    # a grid a little past whole rounds of 512 workgroups: the whole rounds
+    # unsplit, the leftover blocks split over every slot (the workspace holds
+    # kp partials of all of N)
+    assert splits(16, 5120, 32768, 4) == 1       # 512 blocks: exactly one round
+    assert splits(16, 5120, 34816, 4) == 16      # 544: 512 whole + 32 x 16 splits
+    assert splits(16, 5120, 40960, 4) == 4       # 640: 512 whole + 128 x 4
+    assert splits(16, 5120, 49152, 4) == 1       # 768: the leftover is half a round
+    assert splits(16, 5120, 512 * 64 + 6 * 64 - 51, 4) == 20  # 518: 6 x 20 (one step each)
+    assert splits(32, 5120, 34816, 4) == 16      # two activation blocks, same slots
+    ns = (ctypes.c_int64 * 2)(17408, 17408)      # fused gate/up: the 544-block grid
+    ws = lib.dfmi_qmm_multi_workspace_bytes(16, 5120, ns, 2, 64, 4)
+    assert ws == 65536 + 16 * 16 * 544 * 64 * 4

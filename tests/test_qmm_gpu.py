@@ -75,6 +75,36 @@ def test_layer_shapes_other_m(dev, M, K, N):
     _check(_run(dev, x, w_q, s, b, 64), x, w_q, s, b, 64)
 
 
+@pytest.mark.parametrize("M,K,N", [
+    (16, 5120, 34816),                 # 544 blocks: 512 whole + 32 blocks x 16 splits
+    (32, 5120, 34816),                 # the same plan with two activation blocks
+    (16, 5120, 512 * 64 + 6 * 64 - 51),  # 518 blocks, ragged: 6 blocks x 20 one-step splits
+    (16, 2048, 40960)])                # 640 blocks: 512 whole + 128 x 4
+def test_whole_rounds_then_split_tail(dev, M, K, N):
+    """Grids just past whole rounds of 512 workgroups: the whole rounds run
+    unsplit, the leftover blocks split over every slot."""
+    x, w_q, s, b = make_qmm_case(M, K, N, 64, seed=K + N + M + 1)
+    _check(_run(dev, x, w_q, s, b, 64), x, w_q, s, b, 64)
+
+
+def test_split_tail_closed_form_exact(dev):
+    # the same dyadic construction as test_closed_form_exact on a 518-block
+    # grid: unsplit blocks and one-step splits summed by the last arriver
+    # must both be bit-exact
+    rng = np.random.default_rng(47)
+    M, K, N, gs = 16, 5120, 512 * 64 + 6 * 64 - 51, 64
+    q = rng.integers(0, 16, size=(N, K))
+    w_q = oracle.pack(q, 4)
+    s = oracle.f32_to_bf16_bits(np.full((N, K // gs), 0.125, np.float32))
+    b = oracle.f32_to_bf16_bits(np.full((N, K // gs), -1.0, np.float32))
+    xf = np.zeros((M, K), np.float32)
+    for m in range(M):
+        xf[m, rng.choice(K, size=6, replace=False)] = rng.choice([-1.0, 1.0], size=6)
+    x = oracle.f32_to_bf16_bits(xf)
+    want = oracle.quantized_matmul(x, w_q, s, b, group_size=gs, out_dtype="bf16")
+    assert np.array_equal(_run(dev, x, w_q, s, b, gs), want)
+
+
 @pytest.mark.parametrize("M", [1, 4, 8, 12, 15, 17, 24, 32, 48, 80])
 def test_m_sweep(dev, M):
     x, w_q, s, b = make_qmm_case(M, 2048, 768, 64, seed=100 + M)
