@@ -27,20 +27,23 @@
 // (segment s - 1's buffer is then free), so it is in flight while segment s
 // computes and its wait is normally already satisfied.
 //
-// Work partition (stream-K inside each XCD): workgroup g runs on XCD g % 8
-// (the hardware's round-robin dispatch).  XCD x owns the whole blocks
-// [x B / 8, (x + 1) B / 8) and their T_x = B_x S block-steps; its
-// G_x = min(32, T_x) workgroups take contiguous ranges
-// [q T_x / G_x, (q + 1) T_x / G_x).  Blocks
-// wholly inside a range are stored directly; a range starts and ends with at
-// most one partial block each, and every workgroup of a partial block is on
-// one XCD, so the exchange stays in that XCD's L2.  A partial block's fp32
+// Work partition (stream-K in eight groups): group x = the workgroups g with
+// g % 8 = x (the XCD that round-robin dispatch would give them; measured
+// placement does not always follow it, and nothing relies on it) owns the
+// whole blocks [x B / 8, (x + 1) B / 8) and their T_x = B_x S block-steps;
+// its G_x = min(32, T_x) workgroups take contiguous ranges
+// [q T_x / G_x, (q + 1) T_x / G_x).  Blocks wholly inside a range are stored
+// directly; a range starts and ends with at most one partial block each, all
+// of a partial block's workgroups being in one group.  A partial block's fp32
 // tile goes to the workspace (slot 0 for the workgroup's first unit, slot 1
-// for its last) with agent-scope stores; at its end the workgroup waits for
-// its own stores and bumps the counters of its partial blocks; the last
-// workgroup to arrive sums the parts in workgroup order (deterministic) with
-// agent-scope loads and writes y.  Nothing is in flight then, so the exchange
-// never drains the pipeline.
+// for its last) with agent-scope atomic stores; at its end the workgroup
+// waits for its own stores (vmcnt 0) and bumps the counters of its partial
+// blocks with agent-scope RMWs; the last workgroup to arrive (its RMW returned
+// the final count) sums the parts in workgroup order (deterministic) with
+// agent-scope atomic loads issued after that return, and writes y.
+// Agent-scope atomic accesses are coherent across the XCDs' L2s, so the
+// exchange is correct wherever the workgroups run.  Nothing is in flight at
+// the end, so the exchange never drains the pipeline.
 //
 // Per-unit epilogue: the 8 wavefronts' partial tiles are summed through the
 // window buffer of the segment that just ended (every wavefront has read its

@@ -194,9 +194,11 @@ __device__ inline void stream_unit_of(int L, int whole, int kp, int xcd_map, int
   L -= whole;
   kpw = kp;
   if (xcd_map) {
-    // consecutive workgroup ids go to different XCDs (id & 7): give the kp
-    // splits of one block to one XCD so the block's partials and counter
-    // stay in one L2
+    // round-robin dispatch sends consecutive workgroup ids to different XCDs
+    // (id & 7): give the kp splits of one block ids of one residue so that,
+    // where placement follows it, the block's partials and counter stay in
+    // one L2 (correctness does not depend on it: the exchange is agent-scope
+    // atomics)
     const int xcd = L & 7, j = L >> 3;
     const int nbl = j / kp;
     kpi = j - nbl * kp;
