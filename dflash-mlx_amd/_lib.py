@@ -37,9 +37,17 @@ class QmmTuning(ctypes.Structure):
 
 
 class QmmSegment(ctypes.Structure):
-    """dfmi_qmm_segment: one matrix of a shared-activation launch."""
+    """dfmi_qmm_segment: one matrix of a shared-activation launch (sb_pairs:
+    its pair table or NULL)."""
     _fields_ = [("w_q", ctypes.c_void_p), ("scales", ctypes.c_void_p),
-                ("biases", ctypes.c_void_p), ("y", ctypes.c_void_p), ("N", ctypes.c_int64)]
+                ("biases", ctypes.c_void_p), ("y", ctypes.c_void_p), ("N", ctypes.c_int64),
+                ("sb_pairs", ctypes.c_void_p)]
+
+
+class QmmPlanInfo(ctypes.Structure):
+    """dfmi_qmm_plan_info: the streaming launch a qmm call makes."""
+    _fields_ = [(n, ctypes.c_int) for n in ("streaming", "waves", "k_splits", "whole_blocks",
+                                             "blocks", "workgroups", "pair_streaming")]
 
 
 # name -> (restype, argtypes)
@@ -52,6 +60,12 @@ _SIGNATURES = {
                                   _i64, _i64, _i64, _int, _int, _c_void_p, _size,
                                   ctypes.POINTER(QmmTuning), _c_void_p]),
     "dfmi_qmm_workspace_bytes": (_size, [_i64, _i64, _i64, _int, _int]),
+    "dfmi_qmm_affine_pairs": (_int, [_c_void_p, _int, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                     _c_void_p, _i64, _i64, _i64, _int, _int, _c_void_p, _size,
+                                     ctypes.POINTER(QmmTuning), _c_void_p]),
+    "dfmi_sb_pairs": (_int, [_c_void_p, _c_void_p, _int, _i64, _i64, _c_void_p, _c_void_p]),
+    "dfmi_qmm_plan": (_int, [_i64, _i64, ctypes.POINTER(ctypes.c_int64), _int, _int, _int,
+                             ctypes.POINTER(QmmTuning), ctypes.POINTER(QmmPlanInfo)]),
     "dfmi_qmm_kernel_name": (ctypes.c_char_p, [_i64, _i64, _i64, _int, _int,
                                                ctypes.POINTER(QmmTuning)]),
     "dfmi_qmm_workspace_bytes_ex": (_size, [_i64, _i64, _i64, _int, _int,

@@ -7,6 +7,7 @@ arithmetic on the verify path happens in libdfmi.so.
 from __future__ import annotations
 
 import threading
+import weakref
 
 import torch
 
@@ -101,3 +102,59 @@ def workspace(device: torch.device, nbytes: int, kind: str = "qmm") -> tuple[int
     base = buf.data_ptr()
     aligned = (base + 255) // 256 * 256
     return aligned, buf.numel() - (aligned - base)
+
+
+def pair_shape(M: int, K: int, N: int, group_size: int, bits: int) -> bool:
+    """Shapes whose streaming plan can take a pair table (``dfmi_qmm_affine_pairs``):
+    4-bit, gs 64 / 128, M <= 16, whole 256-k steps (mirrors the library's rule)."""
+    return (int(bits) == 4 and int(group_size) in (64, 128) and 1 <= int(M) <= 16
+            and int(K) % 256 == 0 and int(K) % (8 * int(group_size)) == 0
+            and (int(N) + 63) // 64 <= 16384)
+
+
+def build_sb_pairs(scales: torch.Tensor, biases: torch.Tensor) -> torch.Tensor:
+    """The ``[K/gs][N]`` uint32 pair table of a layer (``dfmi_sb_pairs``), on
+    the current stream."""
+    N, G = int(scales.shape[-2]), int(scales.shape[-1])
+    pairs = torch.empty((G, N), dtype=torch.int32, device=scales.device)
+    lib = _lib.load()
+    status = lib.dfmi_sb_pairs(scales.data_ptr(), biases.data_ptr(), dtype_code(scales.dtype),
+                               N, G, pairs.data_ptr(), stream_ptr(scales.device))
+    _lib.check(status, "dfmi_sb_pairs")
+    return pairs
+
+
+class _PairCache:
+    """Pair tables of the (scales, biases) tensors the functional operators
+    see, built on first use and kept while the scales tensor lives.  An entry
+    is valid only for the same two tensor objects at the same versions (an
+    in-place update rebuilds it).  Nothing is built during graph capture: the
+    caller then runs without a table (same plan, bit-identical result)."""
+
+    def __init__(self):
+        self._lock = threading.Lock()
+        self._entries: dict[int, tuple] = {}
+
+    def _drop(self, key: int):
+        with self._lock:
+            self._entries.pop(key, None)
+
+    def get(self, scales: torch.Tensor, biases: torch.Tensor):
+        key = id(scales)
+        ver = (scales._version, biases._version)
+        with self._lock:
+            ent = self._entries.get(key)
+        if ent is not None:
+            sref, bref, ever, pairs = ent
+            if sref() is scales and bref() is biases and ever == ver:
+                return pairs
+        if torch.cuda.is_current_stream_capturing():
+            return None
+        pairs = build_sb_pairs(scales, biases)
+        sref = weakref.ref(scales, lambda _r, k=key: self._drop(k))
+        with self._lock:
+            self._entries[key] = (sref, weakref.ref(biases), ver, pairs)
+        return pairs
+
+
+PAIRS = _PairCache()

@@ -159,7 +159,7 @@ struct StreamArgs {
   int kp;
   int n_blocks;
   int xcd_map;
-  int pstride;  // columns of a partial row: N (one matrix) or 64 x n_blocks
+  int pstride;  // columns of a partial row: 64 x (n_blocks - whole)
   int whole;    // blocks [0, whole) run unsplit, one workgroup each; the rest kp-way split
 };
 
@@ -173,6 +173,7 @@ struct StreamSeg {
   uint16_t* y;
   int N;
   int blk0;
+  const uint32_t* t;  // [K/GS][N] (scale, bias) pairs (pair-streaming kernels), or null
 };
 
 struct StreamSegs {
@@ -210,17 +211,19 @@ __device__ inline void stream_unit_of(int L, int whole, int kp, int xcd_map, int
   nb += whole;
 }
 
-// Block nb (of matrix g), K split kpi of kp.
-template <typename Tag, int GS, int MT, int WV, int BITS, int SBPC>
+// Block nb (of matrix g), K split kpi of kp.  TSB: scales and biases come
+// from g.t, the pair table, one step at a time.
+template <typename Tag, int GS, int MT, int WV, int BITS, int SBPC, bool TSB>
 __device__ __forceinline__ void qmm_stream_body(const StreamArgs& a, const StreamSeg& g, int nb,
                                                 int kpi, int kp) {
-  using S = Stream<Tag, GS, MT, WV, SBPC, BITS>;
+  using S = Stream<Tag, GS, MT, WV, SBPC, BITS, 1, TSB>;
   constexpr int kThreads = 64 * WV;
   typename S::Ctx cx;
   cx.x = buffer_rsrc(a.x, (uint32_t)a.M * (uint32_t)a.K * 2u);
   cx.w = buffer_rsrc(g.w, (uint32_t)g.N * (uint32_t)(a.K / 8 * BITS));
   cx.s = buffer_rsrc(g.s, (uint32_t)g.N * (uint32_t)(a.K / GS) * 2u);
   cx.b = buffer_rsrc(g.b, (uint32_t)g.N * (uint32_t)(a.K / GS) * 2u);
+  if constexpr (TSB) cx.t = buffer_rsrc(g.t, (uint32_t)g.N * (uint32_t)(a.K / GS) * 4u);
   cx.K = a.K;
   cx.M = a.M;
   cx.N = g.N;
@@ -272,8 +275,9 @@ __device__ __forceinline__ void qmm_stream_body(const StreamArgs& a, const Strea
       if (mi[q] < a.M && ni[q] < g.N) g.y[(int64_t)mi[q] * g.N + ni[q]] = Num<Tag>::f2h(v[q]);
     return;
   }
-  // this matrix's partial columns start at 64 blk0
-  float* part = a.partials + (int64_t)kpi * a.M * a.pstride + (int64_t)g.blk0 * S::NB;
+  // split blocks only (nb >= whole) have partial columns: block nb's are
+  // 64 (nb - whole) + row, so this matrix's start at 64 (blk0 - whole)
+  float* part = a.partials + (int64_t)kpi * a.M * a.pstride + (int64_t)(g.blk0 - a.whole) * S::NB;
 #pragma unroll
   for (int q = 0; q < PER; ++q)
     if (mi[q] < a.M && ni[q] < g.N)
@@ -289,8 +293,8 @@ __device__ __forceinline__ void qmm_stream_body(const StreamArgs& a, const Strea
   stage_barrier<0>();
   if (!*s_last) return;
   // Sum the kp partials of this thread's outputs in split order.  The
-  // device-coherent loads of four splits x PER outputs are issued together
-  // (one memory round trip per four splits, not one per load).
+  // device-coherent loads of eight splits x PER outputs are issued together
+  // (one memory round trip per eight splits, not one per load).
   float sum[PER];
   int64_t off[PER];
   bool ok[PER];
@@ -298,15 +302,15 @@ __device__ __forceinline__ void qmm_stream_body(const StreamArgs& a, const Strea
   for (int q = 0; q < PER; ++q) {
     sum[q] = 0.f;
     ok[q] = mi[q] < a.M && ni[q] < g.N;
-    off[q] = ok[q] ? (int64_t)mi[q] * a.pstride + (int64_t)g.blk0 * S::NB + ni[q] : 0;
+    off[q] = ok[q] ? (int64_t)mi[q] * a.pstride + (int64_t)(g.blk0 - a.whole) * S::NB + ni[q] : 0;
   }
   const int64_t split = (int64_t)a.M * a.pstride;
-  for (int q0 = 0; q0 < kp; q0 += 4) {
+  for (int q0 = 0; q0 < kp; q0 += 8) {
     // unconditional loads (a split past kp re-reads the last one and is
     // dropped), so the block is straight-line code with one wait
-    float t[4][PER];
+    float t[8][PER];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < 8; ++j) {
       const int64_t base = (int64_t)min(q0 + j, kp - 1) * split;
 #pragma unroll
       for (int q = 0; q < PER; ++q)
@@ -314,7 +318,7 @@ __device__ __forceinline__ void qmm_stream_body(const StreamArgs& a, const Strea
                                     __HIP_MEMORY_SCOPE_AGENT);
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < 8; ++j)
 #pragma unroll
       for (int q = 0; q < PER; ++q) sum[q] += (q0 + j < kp) ? t[j][q] : 0.f;
   }
@@ -330,8 +334,68 @@ struct StreamPlan {
   int whole;  // blocks run unsplit ahead of the kp-way split ones
   int bits;  // 4 or 8
   int sbpc;  // scale / bias window pieces (8-bit with 8 wavefronts: 8, to fit LDS)
+  int tsb;   // the pair-streaming kernel runs this plan when the pair tables are given
   size_t ws_bytes;
 };
+
+constexpr int kCUs = 256;        // MI355X compute units
+constexpr int kTsbPerCU = 3;     // 51 KB pair-streaming workgroups resident per CU
+
+// Shapes with a pair-streaming plan: 4-bit, gs 64 / 128, one activation
+// block, whole 256-k steps (and a split's K range within the window of the
+// kernel that runs the same plan without pair tables).
+static bool tsb_shape(int64_t M, int64_t K, int64_t N, int gs, int bits) {
+  return bits == 4 && (gs == 64 || gs == 128) && M >= 1 && M <= 16 && K % 256 == 0 &&
+         K % (8 * gs) == 0 && (N + kStreamRows - 1) / kStreamRows <= kMaxCounters;
+}
+
+// The automatic plan of a pair-streaming shape: 4 wavefronts, 256-k steps,
+// up to three 51 KB workgroups per CU (768 slots).  Measured on MI355X (M =
+// 16, 27B- and 9B-class shapes, lm_head):
+//  * >= 768 blocks: whole blocks; the last partial round's blocks (at most a
+//    quarter round) split over every slot;
+//  * 512..767 blocks: two whole blocks per CU and the rest split into at most
+//    one piece per CU, so every CU streams the same bytes (5120 x 34816:
+//    27.3 us, all whole 31.2 us);
+//  * 256..511 blocks: whole blocks (one or two per CU);
+//  * fewer: K split so that one workgroup per CU runs (kp = 256 / blocks),
+//    two per CU when a split would still stream >= 12 steps (5120 x 5120:
+//    kp 3 9.1 us, kp 9 12.3 us; 17408 x 5120: kp 6 16.8 us, kp 3 17.5 us):
+//    more, shorter splits pay more fills and exchanges than they gain.
+// The same plan runs on the window kernel when no pair tables are given
+// (80 KB workgroups, two per CU), so both give bit-identical results.
+static void plan_tsb(int64_t M, int64_t K, int64_t N, int gs, StreamPlan& p) {
+  p.bits = 4;
+  p.MT = 1;
+  p.WV = 4;
+  p.tsb = 1;
+  p.sbpc = kSbPieces;
+  p.n_blocks = (int)((N + kStreamRows - 1) / kStreamRows);
+  p.chunks = (int)(K / 256);
+  const int slots = kCUs * kTsbPerCU;
+  const int max_chunks = sb_max_groups(kSbPieces) / (256 / gs);  // window of a split
+  const int kmin = (p.chunks + max_chunks - 1) / max_chunks;
+  const int nb = p.n_blocks;
+  p.whole = 0;
+  p.kp = kmin;
+  if (kmin == 1 && nb >= slots) {
+    const int left = nb % slots;
+    if (left > 0 && 4 * left <= slots) {
+      p.whole = nb - left;
+      p.kp = std::max(1, std::min((int)std::lround((double)slots / left), p.chunks));
+    }
+  } else if (kmin == 1 && nb >= 2 * kCUs) {
+    const int left = nb - 2 * kCUs;
+    p.kp = std::max(1, std::min(kCUs / std::max(1, left), p.chunks));
+    p.whole = (left > 0 && p.kp > 1) ? 2 * kCUs : 0;
+    if (!p.whole) p.kp = 1;
+  } else if (nb < kCUs) {
+    int kp = std::max(1, kCUs / nb);
+    if (p.chunks / kp >= 12) kp = std::max(kp, 2 * kCUs / nb);
+    p.kp = std::max(kmin, std::min(kp, std::max(1, p.chunks / 2)));
+  }
+  p.xcd_map = ((nb - p.whole) % 8 == 0) ? 1 : 0;
+}
 
 // Scale / bias window pieces of the streaming kernel: 16, except for 8-bit
 // weights with 8 wavefronts, whose twice-as-long weight stages leave LDS for
@@ -347,6 +411,16 @@ static int stream_waves(int64_t M, int64_t K, int grid) {
 
 static int plan_stream(int64_t M, int64_t K, int64_t N, int gs, int bits,
                        const dfmi_qmm_tuning* tune, StreamPlan& p) {
+  p.tsb = 0;
+  const bool forced = tune && (tune->k_splits > 0 || tune->waves_per_block > 0);
+  if (!forced && tsb_shape(M, K, N, gs, bits)) {
+    plan_tsb(M, K, N, gs, p);
+    p.grid_x = p.whole + (p.n_blocks - p.whole) * p.kp;
+    p.ws_bytes = p.kp > 1 ? kCounterBytes + (size_t)p.kp * (size_t)M *
+                                                 (size_t)(p.n_blocks - p.whole) * kStreamRows * 4u
+                          : 0;
+    return DFMI_OK;
+  }
   p.bits = bits;
   p.MT = M <= 16 ? 1 : 2;
   p.n_blocks = (int)((N + kStreamRows - 1) / kStreamRows);
@@ -407,28 +481,33 @@ static int plan_stream(int64_t M, int64_t K, int64_t N, int gs, int bits,
     }
   }
   p.grid_x = p.whole + (p.n_blocks - p.whole) * p.kp;
-  p.ws_bytes = p.kp > 1 ? kCounterBytes + (size_t)p.kp * (size_t)M * (size_t)N * 4u : 0;
+  // forced plans of pair-streaming shapes may still run the pair kernel
+  p.tsb = (tsb_shape(M, K, N, gs, bits) && p.WV == 4 && p.MT == 1) ? 1 : 0;
+  p.ws_bytes = p.kp > 1 ? kCounterBytes + (size_t)p.kp * (size_t)M *
+                                               (size_t)(p.n_blocks - p.whole) * kStreamRows * 4u
+                        : 0;
   return DFMI_OK;
 }
 
 // The arguments as scalars, not a by-value struct, so that they are
 // preloaded into SGPRs at wave start (-amdgpu-kernarg-preload-count).
-template <typename Tag, int GS, int MT, int WV, int BITS, int SBPC>
+template <typename Tag, int GS, int MT, int WV, int BITS, int SBPC, bool TSB>
 __global__ __launch_bounds__(64 * WV) void qmm_stream_kernel(
-    const uint16_t* x, const uint32_t* w, const uint16_t* s, const uint16_t* b, uint16_t* y,
-    float* partials, uint32_t* counters, int M, int K, int N, int chunks, int kp, int n_blocks,
-    int xcd_map, int whole) {
+    const uint16_t* x, const uint32_t* w, const uint16_t* s, const uint16_t* b, const uint32_t* t,
+    uint16_t* y, float* partials, uint32_t* counters, int M, int K, int N, int chunks, int kp,
+    int n_blocks, int xcd_map, int whole) {
   int nb, kpi, kpw;
   stream_unit_of(blockIdx.x, whole, kp, xcd_map, nb, kpi, kpw);
   if (nb >= n_blocks) return;  // uniform, before any barrier
-  qmm_stream_body<Tag, GS, MT, WV, BITS, SBPC>(
-      StreamArgs{x, partials, counters, M, K, chunks, kp, n_blocks, xcd_map, N, whole},
-      StreamSeg{w, s, b, y, N, 0}, nb, kpi, kpw);
+  qmm_stream_body<Tag, GS, MT, WV, BITS, SBPC, TSB>(
+      StreamArgs{x, partials, counters, M, K, chunks, kp, n_blocks, xcd_map,
+                 kStreamRows * (n_blocks - whole), whole},
+      StreamSeg{w, s, b, y, N, 0, t}, nb, kpi, kpw);
 }
 
 // Several weight matrices over the same activations (q / k / v, gate / up):
 // their row blocks form one grid.
-template <typename Tag, int GS, int MT, int WV, int BITS, int SBPC>
+template <typename Tag, int GS, int MT, int WV, int BITS, int SBPC, bool TSB>
 __global__ __launch_bounds__(64 * WV) void qmm_stream_multi_kernel(StreamArgs a, StreamSegs m) {
   int nb, kpi, kpw;
   stream_unit_of(blockIdx.x, a.whole, a.kp, a.xcd_map, nb, kpi, kpw);
@@ -438,23 +517,44 @@ __global__ __launch_bounds__(64 * WV) void qmm_stream_multi_kernel(StreamArgs a,
 #pragma unroll
   for (int i = 1; i < kMaxSeg; ++i)
     if (i < m.nseg && nb >= m.seg[i].blk0) g = m.seg[i];
-  qmm_stream_body<Tag, GS, MT, WV, BITS, SBPC>(a, g, nb, kpi, kpw);
+  qmm_stream_body<Tag, GS, MT, WV, BITS, SBPC, TSB>(a, g, nb, kpi, kpw);
 }
 
+// Every matrix of m carries its pair table.
+static bool segs_have_pairs(const StreamSegs& m) {
+  for (int i = 0; i < m.nseg; ++i)
+    if (m.seg[i].N > 0 && !m.seg[i].t) return false;
+  return true;
+}
+
+template <typename Tag, int GS, int MT, int WV, int BITS, bool TSB>
+static void launch_stream_k(const StreamPlan& p, hipStream_t st, const StreamArgs& a,
+                            const StreamSegs& m) {
+  constexpr int SBPC = BITS == 8 && WV == 8 ? 8 : kSbPieces;  // = stream_sb_pieces(BITS, WV)
+  const int lds = Stream<Tag, GS, MT, WV, SBPC, BITS, 1, TSB>::LDS_BYTES;
+  if (m.nseg == 1) {
+    const StreamSeg& g = m.seg[0];
+    hipLaunchKernelGGL((qmm_stream_kernel<Tag, GS, MT, WV, BITS, SBPC, TSB>), dim3(p.grid_x),
+                       dim3(64 * WV), lds, st, a.x, g.w, g.s, g.b, g.t, g.y, a.partials,
+                       a.counters, a.M, a.K, g.N, a.chunks, a.kp, a.n_blocks, a.xcd_map, a.whole);
+  } else {
+    hipLaunchKernelGGL((qmm_stream_multi_kernel<Tag, GS, MT, WV, BITS, SBPC, TSB>),
+                       dim3(p.grid_x), dim3(64 * WV), lds, st, a, m);
+  }
+}
+
+// The pair-streaming kernel when the plan allows it and every matrix has its
+// pair table (4-bit, gs 64 / 128, one activation block, 4 wavefronts).
 template <typename Tag, int GS, int MT, int WV, int BITS>
 static void launch_stream_t(const StreamPlan& p, hipStream_t st, const StreamArgs& a,
                             const StreamSegs& m) {
-  constexpr int SBPC = BITS == 8 && WV == 8 ? 8 : kSbPieces;  // = stream_sb_pieces(BITS, WV)
-  const int lds = Stream<Tag, GS, MT, WV, SBPC, BITS>::LDS_BYTES;
-  if (m.nseg == 1) {
-    const StreamSeg& g = m.seg[0];
-    hipLaunchKernelGGL((qmm_stream_kernel<Tag, GS, MT, WV, BITS, SBPC>), dim3(p.grid_x),
-                       dim3(64 * WV), lds, st, a.x, g.w, g.s, g.b, g.y, a.partials, a.counters,
-                       a.M, a.K, g.N, a.chunks, a.kp, a.n_blocks, a.xcd_map, a.whole);
-  } else {
-    hipLaunchKernelGGL((qmm_stream_multi_kernel<Tag, GS, MT, WV, BITS, SBPC>), dim3(p.grid_x),
-                       dim3(64 * WV), lds, st, a, m);
+  if constexpr (BITS == 4 && GS >= 64 && MT == 1 && WV == 4) {
+    if (p.tsb && segs_have_pairs(m)) {
+      launch_stream_k<Tag, GS, MT, WV, BITS, true>(p, st, a, m);
+      return;
+    }
   }
+  launch_stream_k<Tag, GS, MT, WV, BITS, false>(p, st, a, m);
 }
 
 template <typename Tag, int GS, int BITS>
@@ -489,10 +589,10 @@ static void allow_lds_t() {
   constexpr int SBPC = BITS == 8 && WV == 8 ? 8 : kSbPieces;
   constexpr int lds = Stream<Tag, GS, MT, WV, SBPC, BITS>::LDS_BYTES;
   (void)hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&qmm_stream_kernel<Tag, GS, MT, WV, BITS, SBPC>),
+      reinterpret_cast<const void*>(&qmm_stream_kernel<Tag, GS, MT, WV, BITS, SBPC, false>),
       hipFuncAttributeMaxDynamicSharedMemorySize, lds);
   (void)hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&qmm_stream_multi_kernel<Tag, GS, MT, WV, BITS, SBPC>),
+      reinterpret_cast<const void*>(&qmm_stream_multi_kernel<Tag, GS, MT, WV, BITS, SBPC, false>),
       hipFuncAttributeMaxDynamicSharedMemorySize, lds);
 }
 
@@ -613,7 +713,7 @@ static int launch_streaming(const void* x, int x_dtype, const StreamSegs& m, int
   a.kp = p.kp;
   a.n_blocks = p.n_blocks;
   a.xcd_map = p.xcd_map;
-  a.pstride = (int)n_cols;
+  a.pstride = kStreamRows * (p.n_blocks - p.whole);
   a.whole = p.whole;
   allow_lds_all();
   if (x_dtype == DFMI_BF16) launch_stream<BF16>(gs, p, st, a, m);
@@ -649,6 +749,41 @@ extern "C" size_t dfmi_qmm_workspace_bytes_ex(int64_t M, int64_t K, int64_t N, i
   return p.ws_bytes;
 }
 
+extern "C" int dfmi_qmm_plan(int64_t M, int64_t K, const int64_t* Ns, int nseg, int group_size,
+                             int bits, const dfmi_qmm_tuning* tuning, dfmi_qmm_plan_info* out) {
+  if (!Ns || !out || nseg < 1 || nseg > kMaxSeg || !valid_path(tuning) ||
+      (nseg > 1 && tuning)) {
+    set_error("dfmi_qmm_plan: bad arguments");
+    return DFMI_EINVAL;
+  }
+  for (int i = 0; i < nseg; ++i) {
+    const int rc = validate_qmm(DFMI_BF16, M, K, Ns[i], group_size, bits);
+    if (rc != DFMI_OK) return rc;
+  }
+  *out = dfmi_qmm_plan_info{};
+  int64_t cols = 0;
+  if (nseg == 1) {
+    if (use_persist(M, K, Ns[0], group_size, bits, tuning, nullptr) ||
+        !use_stream(M, K, Ns[0], group_size, bits, tuning))
+      return DFMI_OK;  // not the streaming kernel: streaming = 0
+    cols = Ns[0];
+  } else {
+    cols = multi_stream_cols(M, K, Ns, nseg, group_size, bits);
+    if (cols <= 0) return DFMI_OK;
+  }
+  StreamPlan p;
+  const int rc = plan_stream(M, K, cols, group_size, bits, tuning, p);
+  if (rc != DFMI_OK) return rc;
+  out->streaming = 1;
+  out->waves = p.WV;
+  out->k_splits = p.kp;
+  out->whole_blocks = p.whole;
+  out->blocks = p.n_blocks;
+  out->workgroups = p.grid_x;
+  out->pair_streaming = p.tsb;
+  return DFMI_OK;
+}
+
 extern "C" const char* dfmi_qmm_kernel_name(int64_t M, int64_t K, int64_t N, int group_size,
                                              int bits, const dfmi_qmm_tuning* tuning) {
   if (validate_qmm(DFMI_BF16, M, K, N, group_size, bits) != DFMI_OK || !valid_path(tuning))
@@ -665,11 +800,12 @@ extern "C" size_t dfmi_qmm_workspace_bytes(int64_t M, int64_t K, int64_t N, int 
   return dfmi_qmm_workspace_bytes_ex(M, K, N, group_size, bits, nullptr);
 }
 
-extern "C" int dfmi_qmm_affine_ex(const void* x, int x_dtype, const uint32_t* w_q,
-                                  const void* scales, const void* biases, void* y, int64_t M,
-                                  int64_t K, int64_t N, int group_size, int bits, void* workspace,
-                                  size_t workspace_bytes, const dfmi_qmm_tuning* tuning,
-                                  void* stream) {
+extern "C" int dfmi_qmm_affine_pairs(const void* x, int x_dtype, const uint32_t* w_q,
+                                     const void* scales, const void* biases,
+                                     const uint32_t* sb_pairs, void* y, int64_t M, int64_t K,
+                                     int64_t N, int group_size, int bits, void* workspace,
+                                     size_t workspace_bytes, const dfmi_qmm_tuning* tuning,
+                                     void* stream) {
   int rc = validate_qmm(x_dtype, M, K, N, group_size, bits);
   if (rc != DFMI_OK) return rc;
   if (!valid_path(tuning)) {
@@ -696,8 +832,9 @@ extern "C" int dfmi_qmm_affine_ex(const void* x, int x_dtype, const uint32_t* w_
     set_error("dfmi_qmm: null pointer");
     return DFMI_EINVAL;
   }
-  if (!aligned16(x) || !aligned16(w_q) || !aligned16(scales) || !aligned16(biases)) {
-    set_error("dfmi_qmm: x, w_q, scales and biases must be 16-byte aligned");
+  if (!aligned16(x) || !aligned16(w_q) || !aligned16(scales) || !aligned16(biases) ||
+      (sb_pairs && !aligned16(sb_pairs))) {
+    set_error("dfmi_qmm: x, w_q, scales, biases and sb_pairs must be 16-byte aligned");
     return DFMI_EINVAL;
   }
   if (persist) {
@@ -712,7 +849,8 @@ extern "C" int dfmi_qmm_affine_ex(const void* x, int x_dtype, const uint32_t* w_
   if (use_stream(M, K, N, group_size, bits, tuning)) {
     StreamSegs m{};
     m.seg[0] = StreamSeg{w_q, static_cast<const uint16_t*>(scales),
-                         static_cast<const uint16_t*>(biases), static_cast<uint16_t*>(y), (int)N, 0};
+                         static_cast<const uint16_t*>(biases), static_cast<uint16_t*>(y), (int)N, 0,
+                         sb_pairs};
     m.nseg = 1;
     return launch_streaming(x, x_dtype, m, M, K, N, group_size, bits, tuning, workspace,
                             workspace_bytes, st);
@@ -733,6 +871,15 @@ extern "C" int dfmi_qmm_affine_ex(const void* x, int x_dtype, const uint32_t* w_
   if (x_dtype == DFMI_BF16) launch_tag<BF16>(group_size, p, st, a);
   else launch_tag<F16>(group_size, p, st, a);
   return check_launch("dfmi_qmm_affine");
+}
+
+extern "C" int dfmi_qmm_affine_ex(const void* x, int x_dtype, const uint32_t* w_q,
+                                  const void* scales, const void* biases, void* y, int64_t M,
+                                  int64_t K, int64_t N, int group_size, int bits, void* workspace,
+                                  size_t workspace_bytes, const dfmi_qmm_tuning* tuning,
+                                  void* stream) {
+  return dfmi_qmm_affine_pairs(x, x_dtype, w_q, scales, biases, nullptr, y, M, K, N, group_size,
+                               bits, workspace, workspace_bytes, tuning, stream);
 }
 
 extern "C" int dfmi_qmm_affine(const void* x, int x_dtype, const uint32_t* w_q, const void* scales,
@@ -873,8 +1020,10 @@ extern "C" int dfmi_qmm_affine_multi(const void* x, int x_dtype, const dfmi_qmm_
       set_error("dfmi_qmm_multi: null pointer in segment %d", i);
       return DFMI_EINVAL;
     }
-    if (!aligned16(segs[i].w_q) || !aligned16(segs[i].scales) || !aligned16(segs[i].biases)) {
-      set_error("dfmi_qmm_multi: segment %d: w_q, scales and biases must be 16-byte aligned", i);
+    if (!aligned16(segs[i].w_q) || !aligned16(segs[i].scales) || !aligned16(segs[i].biases) ||
+        (segs[i].sb_pairs && !aligned16(segs[i].sb_pairs))) {
+      set_error("dfmi_qmm_multi: segment %d: w_q, scales, biases and sb_pairs must be 16-byte "
+                "aligned", i);
       return DFMI_EINVAL;
     }
   }
@@ -888,7 +1037,7 @@ extern "C" int dfmi_qmm_affine_multi(const void* x, int x_dtype, const dfmi_qmm_
     for (int i = 0; i < nseg; ++i) {
       m.seg[i] = StreamSeg{segs[i].w_q, static_cast<const uint16_t*>(segs[i].scales),
                            static_cast<const uint16_t*>(segs[i].biases),
-                           static_cast<uint16_t*>(segs[i].y), (int)Ns[i], blk};
+                           static_cast<uint16_t*>(segs[i].y), (int)Ns[i], blk, segs[i].sb_pairs};
       blk += (int)((Ns[i] + kStreamRows - 1) / kStreamRows);
     }
     m.nseg = nseg;
@@ -897,10 +1046,61 @@ extern "C" int dfmi_qmm_affine_multi(const void* x, int x_dtype, const dfmi_qmm_
   }
   // one launch per matrix, in order on the stream (they may share the workspace)
   for (int i = 0; i < nseg; ++i) {
-    const int rc = dfmi_qmm_affine_ex(x, x_dtype, segs[i].w_q, segs[i].scales, segs[i].biases,
-                                      segs[i].y, M, K, segs[i].N, group_size, bits, workspace,
-                                      workspace_bytes, nullptr, stream);
+    const int rc = dfmi_qmm_affine_pairs(x, x_dtype, segs[i].w_q, segs[i].scales,
+                                         segs[i].biases, segs[i].sb_pairs, segs[i].y, M, K,
+                                         segs[i].N, group_size, bits, workspace, workspace_bytes,
+                                         nullptr, stream);
     if (rc != DFMI_OK) return rc;
   }
   return DFMI_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Pair table of the pair-streaming kernels: pairs[g][n] = scales[n][g] |
+// biases[n][g] << 16 (16-bit values of either activation dtype).  Each
+// workgroup transposes a 64 (rows) x 64 (groups) tile through LDS so that
+// both the reads (along groups) and the writes (along rows) are contiguous.
+__global__ __launch_bounds__(256) void sb_pairs_kernel(const uint16_t* s, const uint16_t* b,
+                                                       uint32_t* t, int N, int G) {
+  __shared__ uint32_t tile[64][65];
+  const int n0 = blockIdx.x * 64, g0 = blockIdx.y * 64;
+  for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+    const int r = i / 64, c = i % 64;  // row n0 + r, group g0 + c
+    const int n = n0 + r, g = g0 + c;
+    uint32_t v = 0;
+    if (n < N && g < G) {
+      const int64_t o = (int64_t)n * G + g;
+      v = (uint32_t)s[o] | ((uint32_t)b[o] << 16);
+    }
+    tile[r][c] = v;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+    const int c = i / 64, r = i % 64;  // group g0 + c, row n0 + r
+    const int n = n0 + r, g = g0 + c;
+    if (n < N && g < G) t[(int64_t)g * N + n] = tile[r][c];
+  }
+}
+
+extern "C" int dfmi_sb_pairs(const void* scales, const void* biases, int dtype, int64_t N,
+                             int64_t groups, uint32_t* sb_pairs, void* stream) {
+  if (dtype != DFMI_BF16 && dtype != DFMI_F16) {
+    set_error("dfmi_sb_pairs: dtype %d unsupported (bf16 or f16)", dtype);
+    return DFMI_EINVAL;
+  }
+  if (N < 0 || groups < 0 || N >= (1ll << 31) || groups >= (1ll << 31) ||
+      N * groups * 4 > 0xFFFFFFFFll) {
+    set_error("dfmi_sb_pairs: bad shape N=%lld groups=%lld", (long long)N, (long long)groups);
+    return DFMI_EINVAL;
+  }
+  if (N == 0 || groups == 0) return DFMI_OK;
+  if (!scales || !biases || !sb_pairs) {
+    set_error("dfmi_sb_pairs: null pointer");
+    return DFMI_EINVAL;
+  }
+  const dim3 grid((unsigned)((N + 63) / 64), (unsigned)((groups + 63) / 64));
+  hipLaunchKernelGGL(sb_pairs_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const uint16_t*>(scales), static_cast<const uint16_t*>(biases),
+                     sb_pairs, (int)N, (int)groups);
+  return check_launch("dfmi_sb_pairs");
 }

@@ -121,7 +121,16 @@ __device__ inline uint32_t opaque(uint32_t v) {
 // wavefront k of a group takes the k-th 64-k slice of every step (CK = 64 KW
 // k).  All groups read the same activation stage, so two groups halve the
 // activation bytes per weight byte.
-template <typename Tag, int GS, int MT, int WV, int SBPC = kSbPieces, int BITS = 4, int RW = 1>
+//
+// TSB (pair streaming): instead of a scale / bias window loaded before the
+// first step, every step's DMA brings the (scale, bias) pairs of its groups
+// from a [K/GS][N] table of 32-bit pairs (scale in the low half, bias in the
+// high half; dfmi_sb_pairs builds it): 64 GPC rows x 4 bytes per 64-row block
+// and step, contiguous, so whole-line requests with no window in LDS (51 KB
+// instead of 80 KB with 4 wavefronts: three workgroups per CU).  The
+// arithmetic is the window path's, operation for operation.
+template <typename Tag, int GS, int MT, int WV, int SBPC = kSbPieces, int BITS = 4, int RW = 1,
+          bool TSB = false>
 struct Stream {
   static constexpr int NT = kStreamTiles;   // 16-row tiles per wavefront
   static constexpr int KW = WV / RW;        // wavefronts along k
@@ -170,13 +179,20 @@ struct Stream {
   static constexpr int MAX_GROUPS = sb_max_groups(SBPC);
   static constexpr int SBPC_N = SBPC;         // pieces per row and array
   static constexpr int SBP = 16 * SBPC;        // bytes per row and array
-  static constexpr int SBBUF = 2 * NB * SBP;   // scales, then biases
+  static constexpr int SBBUF = TSB ? 0 : 2 * NB * SBP;   // scales, then biases
+  // TSB: one stage's pairs, [group of the step][row] 32-bit words; every
+  // wavefront brings TPB bytes of them per step (one DMA, TLANES lanes)
+  static_assert(!TSB || (PAIR && BITS == 4), "pair streaming: gs >= 64, 4-bit weights");
+  static constexpr int SBS = TSB ? GPC * NB * 4 : 0;
+  static constexpr int TPB = SBS / WV;
+  static constexpr int TLANES = TPB / 16;
   // Scale / bias region first: its fragment reads use immediate offsets
   // (the ds_read offset field is 16 bits).
   static constexpr int SB_OFF = 0;
   static constexpr int X_OFF = SBBUF;
   static constexpr int W_OFF = X_OFF + DEPTH * XBUF;
-  static constexpr int LDS_BYTES = W_OFF + DEPTH * WBUF;
+  static constexpr int T_OFF = W_OFF + DEPTH * WBUF;
+  static constexpr int LDS_BYTES = T_OFF + DEPTH * SBS;
   static_assert(LDS_BYTES <= 160 * 1024, "LDS");
   // epilogue: [wave][t][mt][reg][lane] floats, aliasing the stages
   static constexpr int RED_FLOATS = NT * MT * 4 * 64;
@@ -186,11 +202,13 @@ struct Stream {
   static constexpr int W_DMA = WBUF / 1024 / WV;    // = 2
   static constexpr int SB_DMA = SBBUF / 1024 / WV;  // 2 SBPC / WV, once per run()
   static constexpr int SB_RPI = 1024 / SBP;         // rows per scale / bias instruction
-  static constexpr int CHUNK_DMA = X_DMA + W_DMA;
+  static constexpr int T_DMA = TSB ? 1 : 0;                 // pair DMA per step (TSB)
+  static constexpr int CHUNK_DMA = X_DMA + W_DMA + T_DMA;
   static_assert(GS == 32 || GS == 64 || GS == 128, "group size");
 
   struct Ctx {
     __amdgpu_buffer_rsrc_t x, w, s, b;  // activations, packed weights, scales, biases
+    __amdgpu_buffer_rsrc_t t;           // TSB: [K/GS][N] (scale, bias) pairs
     // Rows >= split of the block come from a second weight set (row - split):
     // the up projection next to the gate projection of a fused SwiGLU.
     __amdgpu_buffer_rsrc_t w2, s2, b2;
@@ -224,6 +242,8 @@ struct Stream {
     uint32_t sbr;        // scale fragment: row offset (tile 0)
     uint32_t swz;        // scale window swizzle key of this lane's row: col % SBPC
     uint32_t hsel;       // v_perm selector moving this wavefront's 16-bit half to the high half
+    uint32_t tg;         // TSB: byte offset in the pair table of this lane's piece at step 0
+    uint32_t tfo;        // TSB: pair fragment offset inside a stage (tile 0)
   };
 
   // One step's operands of this lane, read from LDS.
@@ -284,6 +304,21 @@ struct Stream {
     L.swz = (uint32_t)(col % SBPC);
     const int half = PAIR ? (((kw * 64) / GS) & 1) : 0;
     L.hsel = half ? 0x03020c0cu : 0x01000c0cu;
+    if constexpr (TSB) {
+      // lane l < TLANES of wavefront w brings stage bytes w TPB + 16 l: group
+      // o / (4 NB) of the step, rows (o % (4 NB)) / 4 .. + 3 (rows past N read
+      // past the table: zeros, never stored); lanes past TLANES are masked off
+      const int o = cx.wave * TPB + 16 * cx.lane;
+      const int grp = o / (4 * NB), row = (o % (4 * NB)) / 4;
+      const int n = cx.n0 + row;
+      L.tg = (cx.lane < TLANES && n < cx.N)
+                 ? ((uint32_t)grp * (uint32_t)cx.N + (uint32_t)n) * 4u
+                 : kNoRow;
+      L.tfo = (uint32_t)(((kw * 64 / GS) * NB + 64 * rg + col) * 4);
+    } else {
+      L.tg = 0;
+      L.tfo = 0;
+    }
     return L;
   }
 
@@ -330,9 +365,17 @@ struct Stream {
     }
   }
 
+  // TSB: step c's pairs (groups c GPC .. c GPC + GPC - 1 of the block's rows)
+  __device__ static inline void issue_t(const Ctx& cx, const Lane& L, int c, int stage) {
+    if (cx.lane < TLANES)
+      dma16(cx.t, L.tg, (uint32_t)c * (uint32_t)(GPC * 4) * (uint32_t)cx.N,
+            dfmi_smem + T_OFF + stage * SBS + cx.wave * TPB);
+  }
+
   __device__ static inline void issue_chunk(const Ctx& cx, const Lane& L, int c, int stage) {
     issue_x(cx, L, c, stage);
     issue_w(cx, L, c, stage);
+    if constexpr (TSB) issue_t(cx, L, c, stage);
   }
 
   // Step c's fragments of this lane from LDS stage `stage`; g0w = first
@@ -356,6 +399,7 @@ struct Stream {
     const uint32_t gr = (uint32_t)(c * GPC + (PAIR ? (kw * 64) / GS : 2 * kw) - g0w);
     const char* sbp = dfmi_smem + SB_OFF + cx.sb_base +
                       (L.sbr + (((gr >> 3) ^ L.swz) << 4) + ((gr & 7) >> 1) * 4);
+    const char* tp = dfmi_smem + (L.tfo + opaque((uint32_t)(T_OFF + stage * SBS)));
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       if constexpr (PAIR && BITS == 4) {
@@ -379,8 +423,13 @@ struct Stream {
         f.w[t][2] = v1.x;
         f.w[t][3] = v1.y;
       }
-      f.sv[t] = *reinterpret_cast<const uint32_t*>(sbp + t * 16 * SBP);
-      f.bv[t] = *reinterpret_cast<const uint32_t*>(sbp + t * 16 * SBP + NB * SBP);
+      if constexpr (TSB) {
+        f.sv[t] = *reinterpret_cast<const uint32_t*>(tp + t * 16 * 4);  // (scale, bias)
+        f.bv[t] = f.sv[t];
+      } else {
+        f.sv[t] = *reinterpret_cast<const uint32_t*>(sbp + t * 16 * SBP);
+        f.bv[t] = *reinterpret_cast<const uint32_t*>(sbp + t * 16 * SBP + NB * SBP);
+      }
     }
   }
 
@@ -422,8 +471,10 @@ struct Stream {
         b1 = dequant_word8<Tag>(f.w[t][2], f.w[t][3], dq);
       }
       if constexpr (PAIR) {
-        const float s = half_of(f.sv[t], L.hsel);
-        const float bq = __builtin_fmaf(-OFFQ, s, half_of(f.bv[t], L.hsel));
+        // window: this wavefront's half of a dword of two groups; TSB: the
+        // pair's low (scale) and high (bias) halves
+        const float s = half_of(f.sv[t], TSB ? 0x01000c0cu : L.hsel);
+        const float bq = __builtin_fmaf(-OFFQ, s, half_of(f.bv[t], TSB ? 0x03020c0cu : L.hsel));
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
           const f32x4 p = Num<Tag>::mma(f.x[mt][1], b1, Num<Tag>::mma(f.x[mt][0], b0, zero4()));
@@ -483,7 +534,7 @@ struct Stream {
     const Lane L = lane_setup(cx);
     const int piece0 = (c0 * GPC) >> 3;
     const int g0w = piece0 * 8;
-    issue_sb(cx, piece0, ((c1 * GPC + 7) >> 3) - piece0);
+    if constexpr (!TSB) issue_sb(cx, piece0, ((c1 * GPC + 7) >> 3) - piece0);
     issue_chunk(cx, L, c0, 0);
 #pragma unroll
     for (int k = 1; k < DEPTH; ++k)

@@ -180,8 +180,23 @@ def _build_dispatch(obj: VerifyQuantizedLinear, *, enable_qmm: Optional[bool] = 
         s_c = _runtime.aligned_contiguous(obj.scales)
         b_c = _runtime.aligned_contiguous(obj.biases)
         kernel_dtypes = (torch.bfloat16, torch.float16)
+        # the (scale, bias) pair table of the streaming plans, built once per
+        # module on its first GPU call (or by prewarm_verify_kernels), like
+        # the reference's precomputed route; the launch plan and the result
+        # do not depend on it, so a call under graph capture before it exists
+        # runs without it
+        pair_state = [None, obj.scales.dtype in kernel_dtypes and
+                      _runtime.pair_shape(16, K, N, gs, bits)]
+
+        def pairs_of():
+            if pair_state[0] is None and pair_state[1]:
+                if torch.cuda.is_current_stream_capturing():
+                    return None
+                pair_state[0] = _runtime.build_sb_pairs(s_c, b_c)
+            return pair_state[0]
 
         object.__setattr__(obj, "_packed", (w_c, s_c, b_c))
+        object.__setattr__(obj, "_pairs_of", pairs_of)
 
         def call(x: torch.Tensor) -> torch.Tensor:
             orig = x.shape
@@ -193,7 +208,8 @@ def _build_dispatch(obj: VerifyQuantizedLinear, *, enable_qmm: Optional[bool] = 
                 else:
                     x2 = _runtime.aligned_contiguous(x.reshape(m, orig[-1]))
                     tuning = m16_tuning if m == 16 else None
-                    y = qmm_launch(x2, w_c, s_c, b_c, N, gs, bits, tuning).reshape(*orig[:-1], N)
+                    y = qmm_launch(x2, w_c, s_c, b_c, N, gs, bits, tuning,
+                                   pairs=pairs_of()).reshape(*orig[:-1], N)
             else:
                 y = _stock(x)
             return y + bias if bias is not None else y
@@ -230,12 +246,15 @@ def _set_module(model: nn.Module, path: str, new: nn.Module) -> None:
 def prewarm_verify_kernels(model: nn.Module, *, input_dtype: torch.dtype = torch.bfloat16) -> int:
     """dflash_mlx/verify_linear.py:311-336: one M=16 (and M=4 when eligible)
     call per unique (K, N, bits, group_size); also sizes this stream's
-    workspace so later calls (and graph captures) do not allocate it."""
+    workspace so later calls (and graph captures) do not allocate it, and
+    builds every verify module's pair table."""
     seen: set[tuple] = set()
     warmed = 0
     for _, m in _leaf_modules(model):
         if not isinstance(m, VerifyQuantizedLinear):
             continue
+        if "_pairs_of" in m.__dict__:
+            m._pairs_of()
         K = int(m.weight.shape[1]) * (32 // m.bits)
         N = int(m.weight.shape[0])
         key = (K, N, m.bits, m.group_size)
@@ -278,7 +297,8 @@ class SiblingGroup:
         else:
             x2 = _runtime.aligned_contiguous(x.reshape(m, int(x.shape[-1])))
             first = self.members[0]
-            self._ys = qmm_multi_launch(x2, [mem._packed for mem in self.members],
+            self._ys = qmm_multi_launch(x2, [(*mem._packed, mem._pairs_of())
+                                             for mem in self.members],
                                         first.group_size, first.bits)
             self._key = key
             self._taken = set()

@@ -106,10 +106,27 @@ def _kparts_tuning():
     return _tuning(kp) if kp > 0 else None
 
 
+def _pairs_ptr(M: int, K: int, N: int, group_size: int, bits: int, scales, biases,
+               pairs) -> int:
+    """Device pointer of the pair table a launch passes: the given one, else
+    the functional cache's for shapes whose plan can use it (0: none)."""
+    if pairs is None:
+        if not _runtime.pair_shape(M, K, N, group_size, bits):
+            return 0
+        pairs = _runtime.PAIRS.get(scales, biases)
+        if pairs is None:
+            return 0
+    return pairs.data_ptr()
+
+
 def qmm_launch(x2: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
                N: int, group_size: int, bits: int, tuning=None,
-               out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """One ``dfmi_qmm_affine`` launch on the current stream: ``[M, K] -> [M, N]``."""
+               out: Optional[torch.Tensor] = None,
+               pairs: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """One ``dfmi_qmm_affine_pairs`` launch on the current stream:
+    ``[M, K] -> [M, N]``.  ``pairs`` is the layer's pair table
+    (``_runtime.build_sb_pairs``); when None, the one cached for ``scales`` is
+    used (built on first use).  The result does not depend on it."""
     lib = _lib.load()
     M, K = int(x2.shape[0]), int(x2.shape[1])
     dev = x2.device
@@ -117,9 +134,10 @@ def qmm_launch(x2: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: 
     tptr = ctypes.byref(tuning) if tuning is not None else None
     need = int(lib.dfmi_qmm_workspace_bytes_ex(M, K, N, int(group_size), int(bits), tptr))
     ws, ws_bytes = _runtime.workspace(dev, need) if need else (0, 0)
-    status = lib.dfmi_qmm_affine_ex(
+    tp = _pairs_ptr(M, K, N, group_size, bits, scales, biases, pairs)
+    status = lib.dfmi_qmm_affine_pairs(
         x2.data_ptr(), _runtime.dtype_code(x2.dtype), w.data_ptr(), scales.data_ptr(),
-        biases.data_ptr(), y.data_ptr(), M, K, N, int(group_size), int(bits),
+        biases.data_ptr(), tp, y.data_ptr(), M, K, N, int(group_size), int(bits),
         ws, ws_bytes, tptr, _runtime.stream_ptr(dev))
     _lib.check(status, "dfmi_qmm_affine")
     return y
@@ -128,21 +146,25 @@ def qmm_launch(x2: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: 
 def qmm_multi_launch(x2: torch.Tensor, mats, group_size: int, bits: int,
                      outs=None) -> list:
     """One ``dfmi_qmm_affine_multi`` launch on the current stream: the
-    matrices ``mats = [(w, scales, biases), ...]`` (1..4) share ``x2 [M, K]``;
-    returns ``[y_i [M, N_i]]``."""
+    matrices ``mats = [(w, scales, biases[, pairs]), ...]`` (1..4) share
+    ``x2 [M, K]``; returns ``[y_i [M, N_i]]``.  A matrix without its pair
+    table uses the cached one (see :func:`qmm_launch`)."""
     lib = _lib.load()
     M, K = int(x2.shape[0]), int(x2.shape[1])
     dev = x2.device
     n = len(mats)
     if not 1 <= n <= 4:
         raise ValueError("1..4 matrices per launch")
-    Ns = [int(w.shape[0]) for (w, _, _) in mats]
+    Ns = [int(m[0].shape[0]) for m in mats]
     ys = outs if outs is not None else [torch.empty((M, N), dtype=x2.dtype, device=dev)
                                         for N in Ns]
     segs = (_lib.QmmSegment * n)()
-    for i, ((w, sc, bi), y) in enumerate(zip(mats, ys)):
+    for i, (m, y) in enumerate(zip(mats, ys)):
+        w, sc, bi = m[0], m[1], m[2]
         segs[i].w_q, segs[i].scales, segs[i].biases = w.data_ptr(), sc.data_ptr(), bi.data_ptr()
         segs[i].y, segs[i].N = y.data_ptr(), Ns[i]
+        segs[i].sb_pairs = _pairs_ptr(M, K, Ns[i], group_size, bits, sc, bi,
+                                      m[3] if len(m) > 3 else None)
     ns = (ctypes.c_int64 * n)(*Ns)
     need = int(lib.dfmi_qmm_multi_workspace_bytes(M, K, ns, n, int(group_size), int(bits)))
     ws, ws_bytes = _runtime.workspace(dev, need) if need else (0, 0)

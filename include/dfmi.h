@@ -102,6 +102,53 @@ int dfmi_qmm_affine_ex(const void *x, int x_dtype, const uint32_t *w_q, const vo
                        int group_size, int bits, void *workspace, size_t workspace_bytes,
                        const dfmi_qmm_tuning *tuning, void *stream);
 size_t dfmi_qmm_workspace_bytes(int64_t M, int64_t K, int64_t N, int group_size, int bits);
+
+/*
+ * dfmi_qmm_affine_ex with the layer's pair table as well: sb_pairs
+ * [K/group_size][N] uint32, pair[g][n] = scales[n][g] | biases[n][g] << 16
+ * (built once per weight by dfmi_sb_pairs; 16-byte aligned).  Same call
+ * sites replaced as dfmi_qmm_affine (verify_qmm.py:905-1022,
+ * verify_linear.py:166-175, 190-211, 223-232); the reference's
+ * VerifyQuantizedLinear likewise precomputes per-module launch state
+ * (verify_linear.py:118-223).  With the table, 4-bit gs 64 / 128 calls with
+ * M <= 16 and whole 256-k steps stream the pairs with every step instead of
+ * holding a scale / bias window in LDS, so three workgroups share a CU.  The
+ * launch plan does not depend on sb_pairs: the result is bit-identical to
+ * dfmi_qmm_affine_ex (tuning included) on the same inputs; sb_pairs may be
+ * NULL.
+ */
+int dfmi_qmm_affine_pairs(const void *x, int x_dtype, const uint32_t *w_q, const void *scales,
+                          const void *biases, const uint32_t *sb_pairs, void *y, int64_t M,
+                          int64_t K, int64_t N, int group_size, int bits, void *workspace,
+                          size_t workspace_bytes, const dfmi_qmm_tuning *tuning, void *stream);
+/*
+ * Pair table for dfmi_qmm_affine_pairs / dfmi_qmm_affine_multi: from scales
+ * and biases [N, groups] (dtype DFMI_BF16 or DFMI_F16, the layer's 16-bit
+ * values) to sb_pairs [groups][N] uint32 (scale in the low half, bias in the
+ * high half), on `stream`.  No reference counterpart: a one-time re-layout of
+ * a loaded layer's scales (the reference reads them in place).
+ */
+int dfmi_sb_pairs(const void *scales, const void *biases, int dtype, int64_t N, int64_t groups,
+                  uint32_t *sb_pairs, void *stream);
+/* Host-only plan query (no reference counterpart; for tests, benchmarks
+ * and profiles): the streaming launch dfmi_qmm_affine_ex (nseg = 1, Ns[0] =
+ * N, tuning as given) or dfmi_qmm_affine_multi (nseg 2..4, tuning NULL)
+ * makes for this shape.  streaming = 0 when another kernel runs (the other
+ * fields are then 0).  blocks: 64-row blocks of the grid; whole_blocks: the
+ * first blocks run unsplit, the rest are split k_splits ways; workgroups:
+ * the grid; pair_streaming: the plan runs on the pair-streaming kernel when
+ * pair tables are given. */
+typedef struct dfmi_qmm_plan_info {
+  int streaming;
+  int waves;
+  int k_splits;
+  int whole_blocks;
+  int blocks;
+  int workgroups;
+  int pair_streaming;
+} dfmi_qmm_plan_info;
+int dfmi_qmm_plan(int64_t M, int64_t K, const int64_t *Ns, int nseg, int group_size, int bits,
+                  const dfmi_qmm_tuning *tuning, dfmi_qmm_plan_info *out);
 /* Host-only plan query (no reference counterpart; for benchmarks and
  * profiles): name of the kernel dfmi_qmm_affine_ex would launch for this
  * shape, "qmm_persist_kernel", "qmm_stream_kernel", "qmm_dense_kernel" or
@@ -156,6 +203,7 @@ typedef struct dfmi_qmm_segment {
   const void *biases;
   void *y;
   int64_t N;
+  const uint32_t *sb_pairs; /* pair table (see dfmi_qmm_affine_pairs) or NULL */
 } dfmi_qmm_segment;
 int dfmi_qmm_affine_multi(const void *x, int x_dtype, const dfmi_qmm_segment *segs, int nseg,
                           int64_t M, int64_t K, int group_size, int bits, void *workspace,

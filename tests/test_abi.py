@@ -146,38 +146,70 @@ def test_workspace_queries(lib):
     assert lib.dfmi_lmhead_workspace_bytes(16) >= 256 + 8 * 16
 
 
-def test_streaming_split_plans(lib):
-    """The streaming matmul's K-split plan, read back through the workspace
-    query (65536 counter bytes + kp fp32 partials of [M, N] when kp > 1)."""
-    def splits(M, K, N, bits):
-        ws = lib.dfmi_qmm_workspace_bytes(M, K, N, 64, bits)
-        if ws == 0:
-            return 1
-        kp, rem = divmod(ws - 65536, M * N * 4)
-        assert rem == 0, ws
-        return kp
+def _plan(lib, M, K, Ns, bits=4, gs=64, tuning=None):
+    """(waves, k_splits, whole_blocks, workgroups, pair_streaming) of the
+    streaming launch, and the workspace bytes the matching query reports."""
+    from dflash_mlx_amd import _lib
+    ns = (ctypes.c_int64 * len(Ns))(*Ns)
+    info = _lib.QmmPlanInfo()
+    tptr = ctypes.byref(tuning) if tuning is not None else None
+    assert lib.dfmi_qmm_plan(M, K, ns, len(Ns), gs, bits, tptr, ctypes.byref(info)) == 0
+    assert info.streaming == 1
+    if len(Ns) == 1:
+        ws = lib.dfmi_qmm_workspace_bytes_ex(M, K, Ns[0], gs, bits, tptr)
+    else:
+        ws = lib.dfmi_qmm_multi_workspace_bytes(M, K, ns, len(Ns), gs, bits)
+    # counters + kp fp32 partials of the split blocks' 64 rows
+    split_rows = 64 * (info.blocks - info.whole_blocks)
+    assert ws == (65536 + info.k_splits * M * split_rows * 4 if info.k_splits > 1 else 0)
+    assert info.workgroups == info.whole_blocks + (info.blocks - info.whole_blocks) * info.k_splits
+    return info.waves, info.k_splits, info.whole_blocks, info.workgroups, info.pair_streaming
 
-    # M = 16, 4-bit: one 8-wavefront workgroup per CU, ~256 workgroups
-    assert splits(16, 4096, 4096, 4) == 4
-    assert splits(16, 12288, 4096, 4) == 4
-    assert splits(16, 4096, 12288, 4) == 1
-    # M = 17..32, 4-bit: two workgroups per CU, splits toward 512 workgroups
-    # while each split keeps >= 8 steps of 256 k
-    assert splits(32, 17408, 5120, 4) == 6
-    assert splits(32, 5120, 5120, 4) == 3
-    assert splits(32, 5120, 17408, 4) == 1
+
+def test_streaming_split_plans(lib):
+    """The streaming matmul's launch plans, read back through the plan query
+    (and checked against the workspace query)."""
+    # M <= 16, 4-bit, gs 64: pair-streaming plans, 4 wavefronts, up to three
+    # workgroups per CU.  Fewer than 256 blocks: one workgroup per CU, two
+    # when a split would still stream >= 12 steps of 256 k.
+    assert _plan(lib, 16, 4096, [4096]) == (4, 4, 0, 256, 1)
+    assert _plan(lib, 16, 5120, [5120]) == (4, 3, 0, 240, 1)
+    assert _plan(lib, 16, 5120, [5120, 1024, 1024]) == (4, 2, 0, 224, 1)  # 27B q/k/v
+    assert _plan(lib, 16, 17408, [5120]) == (4, 6, 0, 480, 1)   # 68 steps: 2 per CU
+    assert _plan(lib, 16, 12288, [4096]) == (4, 8, 0, 512, 1)
+    assert _plan(lib, 8, 12288, [4096]) == (4, 8, 0, 512, 1)    # any M <= 16
+    # a split's K range stays within one scale window (120 groups): 68 steps
+    # of 4 groups need at least 3 splits, whatever the grid
+    assert _plan(lib, 16, 17408, [40960])[1:3] == (3, 0)
+    # 256..511 blocks: whole; 512..767: two whole blocks per CU, the rest one
+    # piece per CU; >= 768: whole rounds, the last partial round split
+    assert _plan(lib, 16, 4096, [12288, 12288]) == (4, 1, 0, 384, 1)   # 9B gate/up
+    assert _plan(lib, 16, 5120, [32768]) == (4, 1, 0, 512, 1)
+    assert _plan(lib, 16, 5120, [17408, 17408]) == (4, 8, 512, 512 + 32 * 8, 1)  # 27B gate/up
+    assert _plan(lib, 16, 5120, [40960]) == (4, 2, 512, 512 + 128 * 2, 1)
+    assert _plan(lib, 16, 5120, [518 * 64 - 51]) == (4, 20, 512, 512 + 6 * 20, 1)
+    assert _plan(lib, 16, 5120, [151936]) == (4, 11, 2304, 2304 + 70 * 11, 1)  # lm_head rows
+    # gs 128 too; gs 32 and 8-bit weights keep the window plans
+    assert _plan(lib, 16, 5120, [5120], gs=128)[4] == 1
+    assert _plan(lib, 16, 5120, [5120], gs=32)[4] == 0
+    # M = 17..32, 4-bit: two activation blocks, two workgroups per CU,
+    # splits toward 512 workgroups while each keeps >= 8 steps of 256 k;
+    # whole rounds of 512 then a split tail
+    assert _plan(lib, 32, 17408, [5120])[:2] == (4, 6)
+    assert _plan(lib, 32, 5120, [5120])[:2] == (4, 3)
+    assert _plan(lib, 32, 5120, [17408])[:2] == (4, 1)
+    assert _plan(lib, 32, 5120, [34816])[:3] == (4, 16, 512)
     # 8-bit, M = 16: the unsplit 192-block grid runs as 4 wavefronts, 2 splits
-    assert splits(16, 4096, 12288, 8) == 2
-    assert splits(16, 4096, 4096, 8) == 4
-    # a grid a little past whole rounds of 512 workgroups: the whole rounds
-    # unsplit, the leftover blocks split over every slot (the workspace holds
-    # kp partials of all of N)
-    assert splits(16, 5120, 32768, 4) == 1       # 512 blocks: exactly one round
-    assert splits(16, 5120, 34816, 4) == 16      # 544: 512 whole + 32 x 16 splits
-    assert splits(16, 5120, 40960, 4) == 4       # 640: 512 whole + 128 x 4
-    assert splits(16, 5120, 49152, 4) == 1       # 768: the leftover is half a round
-    assert splits(16, 5120, 512 * 64 + 6 * 64 - 51, 4) == 20  # 518: 6 x 20 (one step each)
-    assert splits(32, 5120, 34816, 4) == 16      # two activation blocks, same slots
-    ns = (ctypes.c_int64 * 2)(17408, 17408)      # fused gate/up: the 544-block grid
-    ws = lib.dfmi_qmm_multi_workspace_bytes(16, 5120, ns, 2, 64, 4)
-    assert ws == 65536 + 16 * 16 * 544 * 64 * 4
+    assert _plan(lib, 16, 4096, [12288], bits=8)[:2] == (4, 2)
+    assert _plan(lib, 16, 4096, [4096], bits=8)[:2] == (8, 4)
+    # explicit splits / wavefronts take the window planner; the plan still
+    # runs on the pair kernel when it has 4 wavefronts and one activation block
+    t = _lib_tuning(0, 0, 4, 2)
+    assert _plan(lib, 16, 5120, [5120], tuning=t) == (4, 2, 0, 160, 1)
+    t = _lib_tuning(0, 0, 8, 2)
+    assert _plan(lib, 16, 5120, [5120], tuning=t) == (8, 2, 0, 160, 0)
+
+
+def _lib_tuning(path, tiles, waves, splits):
+    from dflash_mlx_amd import _lib
+    return _lib.QmmTuning(path, tiles, waves, splits)

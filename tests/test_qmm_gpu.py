@@ -76,13 +76,14 @@ def test_layer_shapes_other_m(dev, M, K, N):
 
 
 @pytest.mark.parametrize("M,K,N", [
-    (16, 5120, 34816),                 # 544 blocks: 512 whole + 32 blocks x 16 splits
-    (32, 5120, 34816),                 # the same plan with two activation blocks
-    (16, 5120, 512 * 64 + 6 * 64 - 51),  # 518 blocks, ragged: 6 blocks x 20 one-step splits
-    (16, 2048, 40960)])                # 640 blocks: 512 whole + 128 x 4
+    (16, 5120, 34816),                 # 544 blocks: 512 whole + 32 blocks x 8 pieces
+    (32, 5120, 34816),                 # two activation blocks: 512 whole + 32 x 16 splits
+    (16, 5120, 512 * 64 + 6 * 64 - 51),  # 518 blocks, ragged: 6 blocks x 20 one-step pieces
+    (16, 2048, 40960)])                # 640 blocks: 512 whole + 128 x 2
 def test_whole_rounds_then_split_tail(dev, M, K, N):
-    """Grids just past whole rounds of 512 workgroups: the whole rounds run
-    unsplit, the leftover blocks split over every slot."""
+    """Grids just past 512 blocks: two whole blocks per CU, the leftover
+    blocks split into one piece per CU (M <= 16); M = 17..32: whole rounds of
+    512 workgroups, the leftover blocks split over every slot."""
     x, w_q, s, b = make_qmm_case(M, K, N, 64, seed=K + N + M + 1)
     _check(_run(dev, x, w_q, s, b, 64), x, w_q, s, b, 64)
 
@@ -273,7 +274,7 @@ def test_captured_graph_survives_workspace_growth(dev):
 
     from dflash_mlx_amd import verify_qmm as vq
 
-    M, K, N, gs = 16, 4096, 1024, 64  # K split over 4 workgroups: uses the workspace
+    M, K, N, gs = 16, 4096, 1024, 64  # K split over 8 workgroups: uses the workspace
     x, w_q, s, b = make_qmm_case(M, K, N, gs, seed=21)
     xt, wt, st_, bt = to_dev(x, "bf16", dev), to_dev(w_q, "u32", dev), to_dev(s, "bf16", dev), \
         to_dev(b, "bf16", dev)
@@ -285,7 +286,7 @@ def test_captured_graph_survives_workspace_growth(dev):
     with torch.cuda.graph(graph, stream=stream):
         yg = vq.quantized_matmul(xt, wt, st_, bt, group_size=gs)
     # a larger split-K call on the same stream grows the workspace
-    K2, N2 = 12288, 4096  # 4 splits: 1 MiB of partials against 256 KiB
+    K2, N2 = 12288, 4096  # 8 splits: 2 MiB of partials against 512 KiB
     with torch.cuda.stream(stream):  # (values irrelevant: only the workspace size matters)
         vq.quantized_matmul(torch.zeros((M, K2), dtype=torch.bfloat16, device=dev),
                             torch.zeros((N2, K2 // 8), dtype=torch.int32, device=dev),

@@ -51,7 +51,7 @@ def _both(dev, M, K, N, gs, seed):
 
 
 def test_noalloc_matches_workspace_entry_on_consecutive_calls(dev):
-    # 64 blocks split 4 ways, then a smaller call (16 blocks split 2 ways,
+    # 64 blocks split 4 ways, then a smaller call (16 blocks split 4 ways,
     # ragged N, M = 4) over the same scratch, then the first shape again
     _both(dev, 16, 4096, 4096, 64, seed=11)
     _both(dev, 4, 2048, 1000, 64, seed=12)
