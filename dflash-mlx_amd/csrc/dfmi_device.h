@@ -112,6 +112,32 @@ __device__ inline u32x4 dequant_word4(uint32_t w, const DqConst& dq) {
   return r;
 }
 
+// The same word as an MFMA operand in the slot order (q0, q4, q1, q5, q2, q6,
+// q3, q7): nibbles 4 apart share a 16-bit pair after one shift, so seven VALU
+// operations (three shifts, four v_and_or_b32) and no permutes.  The other
+// operand must hold its 8 k in the same order (kperm_x); the MFMA's sum over
+// the 32 k of a lane group does not depend on which slot holds which k.
+template <typename Tag>
+__device__ inline u32x4 dequant_word4_kperm(uint32_t w, const DqConst& dq) {
+  u32x4 r;
+  r.x = (w & dq.mask) | dq.magic;          // (q0, q4)
+  r.y = ((w >> 4) & dq.mask) | dq.magic;   // (q1, q5)
+  r.z = ((w >> 8) & dq.mask) | dq.magic;   // (q2, q6)
+  r.w = ((w >> 12) & dq.mask) | dq.magic;  // (q3, q7)
+  return r;
+}
+
+// 8 activations in k order (x0 x1 | x2 x3 | x4 x5 | x6 x7) -> the slot order of
+// dequant_word4_kperm (x0 x4 | x1 x5 | x2 x6 | x3 x7): four byte permutes.
+__device__ inline u32x4 kperm_x(u32x4 a) {
+  u32x4 r;
+  r.x = __builtin_amdgcn_perm(a.z, a.x, 0x05040100u);  // (x0, x4)
+  r.y = __builtin_amdgcn_perm(a.z, a.x, 0x07060302u);  // (x1, x5)
+  r.z = __builtin_amdgcn_perm(a.w, a.y, 0x05040100u);  // (x2, x6)
+  r.w = __builtin_amdgcn_perm(a.w, a.y, 0x07060302u);  // (x3, x7)
+  return r;
+}
+
 // Two words of 8-bit values (q0..q3, q4..q7, k order, lowest byte first)
 // -> MFMA operand of 8 16-bit values in k order, exactly:
 //   bf16: q -> fp32 (v_cvt_f32_ubyte), whose high half is the bf16 value

@@ -446,9 +446,21 @@ struct Stream {
     }
   }
 
+  // All-ones MFMA operand held in VGPRs (the empty asm keeps the compiler
+  // from rematerialising it from SGPRs before every use).
+  __device__ static inline u32x4 ones_operand() {
+    u32x4 ones = u32x4{Num<Tag>::ONE2, Num<Tag>::ONE2, Num<Tag>::ONE2, Num<Tag>::ONE2};
+    asm volatile("" : "+v"(ones));
+    return ones;
+  }
+
   __device__ static inline void compute(const Lane& L, const Frag& f, f32x4 (&acc)[NT][MT],
                                         const DqConst& dq) {
-    const u32x4 ones = u32x4{Num<Tag>::ONE2, Num<Tag>::ONE2, Num<Tag>::ONE2, Num<Tag>::ONE2};
+    compute(L, f, acc, dq, u32x4{Num<Tag>::ONE2, Num<Tag>::ONE2, Num<Tag>::ONE2, Num<Tag>::ONE2});
+  }
+
+  __device__ static inline void compute(const Lane& L, const Frag& f, f32x4 (&acc)[NT][MT],
+                                        const DqConst& dq, const u32x4 ones) {
     // group sums of the slice: lane (col, kg) gets X[m = 4 kg + r] in register r
     f32x4 xs[MT][2];
 #pragma unroll
@@ -460,12 +472,20 @@ struct Stream {
         xs[mt][1] = Num<Tag>::mma(f.x[mt][1], ones, zero4());
       }
     }
+    // Product operands: 4-bit weights take the k-permuted dequantisation
+    // (seven VALU operations a word instead of nine), the activations the
+    // same permutation (four permutes a fragment, shared by the NT tiles).
+    u32x4 xa[MT][2];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) xa[mt][j] = BITS == 4 ? kperm_x(f.x[mt][j]) : f.x[mt][j];
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       u32x4 b0, b1;
       if constexpr (BITS == 4) {
-        b0 = dequant_word4<Tag>(f.w[t][0], dq);
-        b1 = dequant_word4<Tag>(f.w[t][1], dq);
+        b0 = dequant_word4_kperm<Tag>(f.w[t][0], dq);
+        b1 = dequant_word4_kperm<Tag>(f.w[t][1], dq);
       } else {
         b0 = dequant_word8<Tag>(f.w[t][0], f.w[t][1], dq);
         b1 = dequant_word8<Tag>(f.w[t][2], f.w[t][3], dq);
@@ -477,7 +497,7 @@ struct Stream {
         const float bq = __builtin_fmaf(-OFFQ, s, half_of(f.bv[t], TSB ? 0x03020c0cu : L.hsel));
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-          const f32x4 p = Num<Tag>::mma(f.x[mt][1], b1, Num<Tag>::mma(f.x[mt][0], b0, zero4()));
+          const f32x4 p = Num<Tag>::mma(xa[mt][1], b1, Num<Tag>::mma(xa[mt][0], b0, zero4()));
 #pragma unroll
           for (int r = 0; r < 4; ++r)
             acc[t][mt][r] = __builtin_fmaf(bq, xs[mt][0][r], __builtin_fmaf(s, p[r], acc[t][mt][r]));
@@ -490,7 +510,7 @@ struct Stream {
           const float bq = __builtin_fmaf(-OFFQ, s, half_of(f.bv[t], sel));
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) {
-            const f32x4 p = Num<Tag>::mma(f.x[mt][j], j ? b1 : b0, zero4());
+            const f32x4 p = Num<Tag>::mma(xa[mt][j], j ? b1 : b0, zero4());
 #pragma unroll
             for (int r = 0; r < 4; ++r)
               acc[t][mt][r] =
@@ -515,15 +535,20 @@ struct Stream {
   // be in flight); step c is in `cur`.
   __device__ static inline void step(const Ctx& cx, const Lane& L, int c, int c1, int stage,
                                      int g0w, Frag& cur, Frag& nxt, f32x4 (&acc)[NT][MT],
-                                     const DqConst& dq) {
+                                     const DqConst& dq, const u32x4 ones) {
     if (c + 1 < c1) {
       wait_steps(min(DEPTH - 2, c1 - c - 2));
       if (c + DEPTH < c1)
         issue_chunk(cx, L, c + DEPTH, stage);  // step c's stage: its fragments are in cur
-      const int st1 = stage == DEPTH - 1 ? 0 : stage + 1;
-      read_frag(cx, L, c + 1, st1, g0w, nxt);
     }
-    compute(L, cur, acc, dq);
+    // The next step's fragments -- read on the last step too (a stage whose
+    // loads have all landed, in bounds, the values unused), so that nxt is
+    // always written here and the two fragment sets need no register copies
+    // between iterations.  The epilogue's barrier orders these reads before
+    // anything reuses the stages.
+    const int st1 = stage == DEPTH - 1 ? 0 : stage + 1;
+    read_frag(cx, L, c + 1, st1, g0w, nxt);
+    compute(L, cur, acc, dq, ones);
   }
 
   // Accumulate steps [c0, c1) (c1 > c0) of this workgroup into acc.  Every
@@ -531,6 +556,7 @@ struct Stream {
   // barriers).  The range covers at most MAX_GROUPS groups.
   __device__ static inline void run(const Ctx& cx, int c0, int c1, f32x4 (&acc)[NT][MT]) {
     const DqConst dq = dq_const<Tag>();
+    const u32x4 ones = ones_operand();
     const Lane L = lane_setup(cx);
     const int piece0 = (c0 * GPC) >> 3;
     const int g0w = piece0 * 8;
@@ -545,12 +571,12 @@ struct Stream {
     read_frag(cx, L, c0, 0, g0w, fa);
     int c = c0, stage = 0;
     for (; c + 1 < c1; c += 2) {
-      step(cx, L, c, c1, stage, g0w, fa, fb, acc, dq);
+      step(cx, L, c, c1, stage, g0w, fa, fb, acc, dq, ones);
       stage = stage == DEPTH - 1 ? 0 : stage + 1;
-      step(cx, L, c + 1, c1, stage, g0w, fb, fa, acc, dq);
+      step(cx, L, c + 1, c1, stage, g0w, fb, fa, acc, dq, ones);
       stage = stage == DEPTH - 1 ? 0 : stage + 1;
     }
-    if (c < c1) step(cx, L, c, c1, stage, g0w, fa, fb, acc, dq);
+    if (c < c1) step(cx, L, c, c1, stage, g0w, fa, fb, acc, dq, ones);
   }
 };
 
