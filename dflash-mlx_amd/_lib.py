@@ -31,9 +31,11 @@ _float = ctypes.c_float
 class QmmTuning(ctypes.Structure):
     """dfmi_qmm_tuning: path (1 general, 2 streaming, 3 persistent), tiles_per_wave,
     waves_per_block (general kernel K split), k_splits (streaming kernel K
-    split across workgroups); 0 = automatic."""
+    split across workgroups), rows_per_block (streaming kernel, 64 or 128);
+    0 = automatic."""
     _fields_ = [("path", ctypes.c_int), ("tiles_per_wave", ctypes.c_int),
-                ("waves_per_block", ctypes.c_int), ("k_splits", ctypes.c_int)]
+                ("waves_per_block", ctypes.c_int), ("k_splits", ctypes.c_int),
+                ("rows_per_block", ctypes.c_int)]
 
 
 class QmmSegment(ctypes.Structure):
@@ -47,7 +49,8 @@ class QmmSegment(ctypes.Structure):
 class QmmPlanInfo(ctypes.Structure):
     """dfmi_qmm_plan_info: the streaming launch a qmm call makes."""
     _fields_ = [(n, ctypes.c_int) for n in ("streaming", "waves", "k_splits", "whole_blocks",
-                                             "blocks", "workgroups", "pair_streaming")]
+                                             "blocks", "workgroups", "pair_streaming",
+                                             "rows_per_block")]
 
 
 # name -> (restype, argtypes)

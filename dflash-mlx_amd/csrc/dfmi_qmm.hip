@@ -212,11 +212,12 @@ __device__ inline void stream_unit_of(int L, int whole, int kp, int xcd_map, int
 }
 
 // Block nb (of matrix g), K split kpi of kp.  TSB: scales and biases come
-// from g.t, the pair table, one step at a time.
-template <typename Tag, int GS, int MT, int WV, int BITS, int SBPC, bool TSB>
+// from g.t, the pair table, one step at a time.  RW = 2: 128-row blocks, two
+// row groups of WV / 2 wavefronts.
+template <typename Tag, int GS, int MT, int WV, int BITS, int SBPC, bool TSB, int RW>
 __device__ __forceinline__ void qmm_stream_body(const StreamArgs& a, const StreamSeg& g, int nb,
                                                 int kpi, int kp) {
-  using S = Stream<Tag, GS, MT, WV, SBPC, BITS, 1, TSB>;
+  using S = Stream<Tag, GS, MT, WV, SBPC, BITS, RW, TSB>;
   constexpr int kThreads = 64 * WV;
   typename S::Ctx cx;
   cx.x = buffer_rsrc(a.x, (uint32_t)a.M * (uint32_t)a.K * 2u);
@@ -241,8 +242,9 @@ __device__ __forceinline__ void qmm_stream_body(const StreamArgs& a, const Strea
     for (int mt = 0; mt < MT; ++mt) acc[t][mt] = zero4();
   S::run(cx, c0, c1, acc);
 
-  // sum the WV wavefronts' partial tiles through LDS (the stages are free:
-  // every DMA has landed and every wavefront is past its last LDS read)
+  // sum the partial tiles of each row group's KW wavefronts through LDS (the
+  // stages are free: every DMA has landed and every wavefront is past its
+  // last LDS read), in k-slice order
   __syncthreads();
   float* red = reinterpret_cast<float*>(dfmi_smem);
   {
@@ -255,18 +257,20 @@ __device__ __forceinline__ void qmm_stream_body(const StreamArgs& a, const Strea
         for (int j = 0; j < 4; ++j) mine[((t * MT + mt) * 4 + j) * 64 + cx.lane] = acc[t][mt][j];
   }
   __syncthreads();
-  constexpr int PER = S::RED_FLOATS / kThreads;
+  constexpr int PER = RW * S::RED_FLOATS / kThreads;
   float v[PER];
   int mi[PER], ni[PER];
 #pragma unroll
   for (int q = 0; q < PER; ++q) {
     const int e = q * kThreads + threadIdx.x;
-    float sum = red[e];
+    const int rg = e / S::RED_FLOATS, eo = e % S::RED_FLOATS;
+    const float* rr = red + rg * S::KW * S::RED_FLOATS + eo;
+    float sum = rr[0];
 #pragma unroll
-    for (int wv = 1; wv < WV; ++wv) sum += red[wv * S::RED_FLOATS + e];
+    for (int k = 1; k < S::KW; ++k) sum += rr[k * S::RED_FLOATS];
     v[q] = sum;
-    const int l = e & 63, j = (e >> 6) & 3, tm = e >> 8;
-    ni[q] = cx.n0 + (tm / MT) * 16 + (l & 15);
+    const int l = eo & 63, j = (eo >> 6) & 3, tm = eo >> 8;
+    ni[q] = cx.n0 + kStreamRows * rg + (tm / MT) * 16 + (l & 15);
     mi[q] = (tm % MT) * 16 + 4 * (l >> 4) + j;
   }
   if (kp == 1) {
@@ -276,7 +280,7 @@ __device__ __forceinline__ void qmm_stream_body(const StreamArgs& a, const Strea
     return;
   }
   // split blocks only (nb >= whole) have partial columns: block nb's are
-  // 64 (nb - whole) + row, so this matrix's start at 64 (blk0 - whole)
+  // NB (nb - whole) + row, so this matrix's start at NB (blk0 - whole)
   float* part = a.partials + (int64_t)kpi * a.M * a.pstride + (int64_t)(g.blk0 - a.whole) * S::NB;
 #pragma unroll
   for (int q = 0; q < PER; ++q)
@@ -335,11 +339,14 @@ struct StreamPlan {
   int bits;  // 4 or 8
   int sbpc;  // scale / bias window pieces (8-bit with 8 wavefronts: 8, to fit LDS)
   int tsb;   // the pair-streaming kernel runs this plan when the pair tables are given
+  int rw;    // 64-row groups per block: 1, or 2 (128-row pair-streaming blocks)
   size_t ws_bytes;
 };
 
-constexpr int kCUs = 256;        // MI355X compute units
-constexpr int kTsbPerCU = 3;     // 51 KB pair-streaming workgroups resident per CU
+constexpr int kCUs = 256;  // MI355X compute units
+// 128-row pair-streaming blocks as the automatic choice where every matrix
+// is a whole number of them
+constexpr bool kAutoRows128 = true;
 
 // Shapes with a pair-streaming plan: 4-bit, gs 64 / 128, one activation
 // block, whole 256-k steps (and a split's K range within the window of the
@@ -349,52 +356,91 @@ static bool tsb_shape(int64_t M, int64_t K, int64_t N, int gs, int bits) {
          K % (8 * gs) == 0 && (N + kStreamRows - 1) / kStreamRows <= kMaxCounters;
 }
 
-// The automatic plan of a pair-streaming shape: 4 wavefronts, 256-k steps,
-// up to three 51 KB workgroups per CU (768 slots).  Measured on MI355X (M =
-// 16, 27B- and 9B-class shapes, lm_head):
-//  * >= 768 blocks: whole blocks; the last partial round's blocks (at most a
+// The matrices of a launch in both block sizes: 64-row blocks, and 128-row
+// blocks when every matrix is a whole number of them (else 0).
+struct StreamGeo {
+  int nb64;
+  int nb128;
+};
+
+static StreamGeo geo_of(const int64_t* Ns, int nseg) {
+  StreamGeo g{0, 0};
+  bool even = true;
+  for (int i = 0; i < nseg; ++i) {
+    g.nb64 += (int)((Ns[i] + kStreamRows - 1) / kStreamRows);
+    even = even && Ns[i] % (2 * kStreamRows) == 0;
+    g.nb128 += (int)(Ns[i] / (2 * kStreamRows));
+  }
+  if (!even) g.nb128 = 0;
+  return g;
+}
+
+// The automatic plan of a pair-streaming shape, 256-k steps.  rw = 1: 64-row
+// blocks, 4 wavefronts, 51 KB, three workgroups per CU; rw = 2: 128-row
+// blocks (two row groups sharing each activation stage, half the activation
+// requests per weight byte), 8 wavefronts, 78 KB, two per CU.  With P
+// workgroups resident per CU (S = 256 P slots), measured on MI355X:
+//  * >= S blocks: whole blocks; the last partial round's blocks (at most a
 //    quarter round) split over every slot;
-//  * 512..767 blocks: two whole blocks per CU and the rest split into at most
-//    one piece per CU, so every CU streams the same bytes (5120 x 34816:
-//    27.3 us, all whole 31.2 us);
-//  * 256..511 blocks: whole blocks (one or two per CU);
-//  * fewer: K split so that one workgroup per CU runs (kp = 256 / blocks),
-//    two per CU when a split would still stream >= 12 steps (5120 x 5120:
-//    kp 3 9.1 us, kp 9 12.3 us; 17408 x 5120: kp 6 16.8 us, kp 3 17.5 us):
-//    more, shorter splits pay more fills and exchanges than they gain.
-// The same plan runs on the window kernel when no pair tables are given
-// (80 KB workgroups, two per CU), so both give bit-identical results.
-static void plan_tsb(int64_t M, int64_t K, int64_t N, int gs, StreamPlan& p) {
+//  * w = blocks / 256 in 1 .. P-1: w whole blocks per CU and the rest split
+//    into at most P - w pieces per CU, so every CU streams the same bytes
+//    (5120 x 34816 at rw 1: 27.3 us, all whole 31.2 us);
+//  * fewer than 256: K split so that one workgroup per CU runs
+//    (kp = 256 / blocks; 5120 x 5120 at rw 1: kp 3 9.0 us, kp 9 12.3 us;
+//    4096 x 24576 at rw 2: kp 1 15.7 us, kp 2 19.2 us): more, shorter
+//    splits pay more fills and exchanges than they gain.
+// The same plan (in 64-row blocks: each 128-row block as two) runs on the
+// window kernel when no pair tables are given (80 KB workgroups, two per
+// CU), so both give bit-identical results.
+static void plan_tsb(int64_t K, const StreamGeo& geo, int gs, int rw, int kp_force,
+                     StreamPlan& p) {
   p.bits = 4;
   p.MT = 1;
-  p.WV = 4;
+  p.rw = rw;
+  p.WV = 4 * rw;
   p.tsb = 1;
   p.sbpc = kSbPieces;
-  p.n_blocks = (int)((N + kStreamRows - 1) / kStreamRows);
+  p.n_blocks = rw == 2 ? geo.nb128 : geo.nb64;
   p.chunks = (int)(K / 256);
-  const int slots = kCUs * kTsbPerCU;
+  const int per_cu = rw == 2 ? 2 : 3;
+  const int slots = kCUs * per_cu;
   const int max_chunks = sb_max_groups(kSbPieces) / (256 / gs);  // window of a split
   const int kmin = (p.chunks + max_chunks - 1) / max_chunks;
   const int nb = p.n_blocks;
   p.whole = 0;
   p.kp = kmin;
-  if (kmin == 1 && nb >= slots) {
+  if (kp_force > 0) {
+    p.kp = std::max(kmin, std::min(kp_force, p.chunks));
+  } else if (kmin == 1 && nb >= slots) {
     const int left = nb % slots;
     if (left > 0 && 4 * left <= slots) {
       p.whole = nb - left;
       p.kp = std::max(1, std::min((int)std::lround((double)slots / left), p.chunks));
     }
-  } else if (kmin == 1 && nb >= 2 * kCUs) {
-    const int left = nb - 2 * kCUs;
-    p.kp = std::max(1, std::min(kCUs / std::max(1, left), p.chunks));
-    p.whole = (left > 0 && p.kp > 1) ? 2 * kCUs : 0;
+  } else if (kmin == 1 && nb >= kCUs) {
+    const int w = nb / kCUs;  // whole blocks per CU, 1 .. per_cu - 1
+    const int left = nb - w * kCUs;
+    p.kp = left > 0 ? std::max(1, std::min((per_cu - w) * kCUs / left, p.chunks)) : 1;
+    p.whole = p.kp > 1 ? w * kCUs : 0;
     if (!p.whole) p.kp = 1;
   } else if (nb < kCUs) {
-    int kp = std::max(1, kCUs / nb);
-    if (p.chunks / kp >= 12) kp = std::max(kp, 2 * kCUs / nb);
+    const int kp = std::max(1, kCUs / nb);
     p.kp = std::max(kmin, std::min(kp, std::max(1, p.chunks / 2)));
   }
   p.xcd_map = ((nb - p.whole) % 8 == 0) ? 1 : 0;
+}
+
+// A 128-row plan as the equivalent 64-row plan (each block as two with the
+// same K splits, so every output is summed in the same order): what the
+// window kernel runs when the pair tables are missing.
+static void plan_as_rows64(StreamPlan& p) {
+  if (p.rw != 2) return;
+  p.rw = 1;
+  p.WV = 4;
+  p.n_blocks *= 2;
+  p.whole *= 2;
+  p.grid_x = p.whole + (p.n_blocks - p.whole) * p.kp;
+  p.xcd_map = ((p.n_blocks - p.whole) % 8 == 0) ? 1 : 0;
 }
 
 // Scale / bias window pieces of the streaming kernel: 16, except for 8-bit
@@ -409,15 +455,46 @@ static int stream_waves(int64_t M, int64_t K, int grid) {
   return (M <= 16 && K % 512 == 0 && grid <= 256) ? 8 : 4;
 }
 
+// Ns / nseg: the matrices of a shared-activation launch (N = their 64-row
+// blocks' columns); nullptr: one matrix of N rows.
 static int plan_stream(int64_t M, int64_t K, int64_t N, int gs, int bits,
-                       const dfmi_qmm_tuning* tune, StreamPlan& p) {
+                       const dfmi_qmm_tuning* tune, StreamPlan& p, const int64_t* Ns = nullptr,
+                       int nseg = 1) {
   p.tsb = 0;
-  const bool forced = tune && (tune->k_splits > 0 || tune->waves_per_block > 0);
-  if (!forced && tsb_shape(M, K, N, gs, bits)) {
-    plan_tsb(M, K, N, gs, p);
+  p.rw = 1;
+  const int64_t one[1] = {N};
+  const StreamGeo geo = geo_of(Ns ? Ns : one, Ns ? nseg : 1);
+  const int rows = tune ? tune->rows_per_block : 0;
+  if (rows != 0 && rows != 64 && rows != 128) {
+    set_error("dfmi_qmm: rows_per_block must be 0, 64 or 128 (got %d)", rows);
+    return DFMI_EINVAL;
+  }
+  const bool waves = tune && tune->waves_per_block > 0;
+  const bool tsb = tsb_shape(M, K, N, gs, bits);
+  if (rows == 128 && (!tsb || !geo.nb128 || waves)) {
+    set_error("dfmi_qmm: 128-row blocks need a pair-streaming shape (4-bit, gs 64 / 128, "
+              "M <= 16, K %% 256 == 0, every N a multiple of 128) and automatic wavefronts");
+    return DFMI_EINVAL;
+  }
+  if (tsb && !waves) {
+    const int kp_force = tune ? tune->k_splits : 0;
+    // 128-row blocks where a workgroup streams 8 steps or more on average (measured
+    // on MI355X: the second row group's stage fill pays off over long
+    // ranges -- 5120 x 34816 24.5 vs 26.7 us, 17408 x 5120 15.6 vs 17.2 us,
+    // 5120 x 151936 95.5 vs 102.7 us -- and loses on short ones: 5120 x
+    // 5120 9.6 vs 9.0 us, 4096 x 4096 8.7 vs 7.9 us)
+    int rw = rows == 128 ? 2 : 1;
+    if (rows == 0 && geo.nb128 && kAutoRows128) {
+      StreamPlan q;
+      plan_tsb(K, geo, gs, 2, kp_force, q);
+      const int grid = q.whole + (q.n_blocks - q.whole) * q.kp;
+      if ((int64_t)q.n_blocks * q.chunks >= 8ll * grid) rw = 2;
+    }
+    plan_tsb(K, geo, gs, rw, kp_force, p);
     p.grid_x = p.whole + (p.n_blocks - p.whole) * p.kp;
     p.ws_bytes = p.kp > 1 ? kCounterBytes + (size_t)p.kp * (size_t)M *
-                                                 (size_t)(p.n_blocks - p.whole) * kStreamRows * 4u
+                                                 (size_t)(p.n_blocks - p.whole) *
+                                                 (size_t)(kStreamRows * p.rw) * 4u
                           : 0;
     return DFMI_OK;
   }
@@ -491,7 +568,7 @@ static int plan_stream(int64_t M, int64_t K, int64_t N, int gs, int bits,
 
 // The arguments as scalars, not a by-value struct, so that they are
 // preloaded into SGPRs at wave start (-amdgpu-kernarg-preload-count).
-template <typename Tag, int GS, int MT, int WV, int BITS, int SBPC, bool TSB>
+template <typename Tag, int GS, int MT, int WV, int BITS, int SBPC, bool TSB, int RW>
 __global__ __launch_bounds__(64 * WV) void qmm_stream_kernel(
     const uint16_t* x, const uint32_t* w, const uint16_t* s, const uint16_t* b, const uint32_t* t,
     uint16_t* y, float* partials, uint32_t* counters, int M, int K, int N, int chunks, int kp,
@@ -499,15 +576,15 @@ __global__ __launch_bounds__(64 * WV) void qmm_stream_kernel(
   int nb, kpi, kpw;
   stream_unit_of(blockIdx.x, whole, kp, xcd_map, nb, kpi, kpw);
   if (nb >= n_blocks) return;  // uniform, before any barrier
-  qmm_stream_body<Tag, GS, MT, WV, BITS, SBPC, TSB>(
+  qmm_stream_body<Tag, GS, MT, WV, BITS, SBPC, TSB, RW>(
       StreamArgs{x, partials, counters, M, K, chunks, kp, n_blocks, xcd_map,
-                 kStreamRows * (n_blocks - whole), whole},
+                 kStreamRows * RW * (n_blocks - whole), whole},
       StreamSeg{w, s, b, y, N, 0, t}, nb, kpi, kpw);
 }
 
 // Several weight matrices over the same activations (q / k / v, gate / up):
 // their row blocks form one grid.
-template <typename Tag, int GS, int MT, int WV, int BITS, int SBPC, bool TSB>
+template <typename Tag, int GS, int MT, int WV, int BITS, int SBPC, bool TSB, int RW>
 __global__ __launch_bounds__(64 * WV) void qmm_stream_multi_kernel(StreamArgs a, StreamSegs m) {
   int nb, kpi, kpw;
   stream_unit_of(blockIdx.x, a.whole, a.kp, a.xcd_map, nb, kpi, kpw);
@@ -517,7 +594,7 @@ __global__ __launch_bounds__(64 * WV) void qmm_stream_multi_kernel(StreamArgs a,
 #pragma unroll
   for (int i = 1; i < kMaxSeg; ++i)
     if (i < m.nseg && nb >= m.seg[i].blk0) g = m.seg[i];
-  qmm_stream_body<Tag, GS, MT, WV, BITS, SBPC, TSB>(a, g, nb, kpi, kpw);
+  qmm_stream_body<Tag, GS, MT, WV, BITS, SBPC, TSB, RW>(a, g, nb, kpi, kpw);
 }
 
 // Every matrix of m carries its pair table.
@@ -527,34 +604,41 @@ static bool segs_have_pairs(const StreamSegs& m) {
   return true;
 }
 
-template <typename Tag, int GS, int MT, int WV, int BITS, bool TSB>
+template <typename Tag, int GS, int MT, int WV, int BITS, bool TSB, int RW>
 static void launch_stream_k(const StreamPlan& p, hipStream_t st, const StreamArgs& a,
                             const StreamSegs& m) {
   constexpr int SBPC = BITS == 8 && WV == 8 ? 8 : kSbPieces;  // = stream_sb_pieces(BITS, WV)
-  const int lds = Stream<Tag, GS, MT, WV, SBPC, BITS, 1, TSB>::LDS_BYTES;
+  const int lds = Stream<Tag, GS, MT, WV, SBPC, BITS, RW, TSB>::LDS_BYTES;
   if (m.nseg == 1) {
     const StreamSeg& g = m.seg[0];
-    hipLaunchKernelGGL((qmm_stream_kernel<Tag, GS, MT, WV, BITS, SBPC, TSB>), dim3(p.grid_x),
+    hipLaunchKernelGGL((qmm_stream_kernel<Tag, GS, MT, WV, BITS, SBPC, TSB, RW>), dim3(p.grid_x),
                        dim3(64 * WV), lds, st, a.x, g.w, g.s, g.b, g.t, g.y, a.partials,
                        a.counters, a.M, a.K, g.N, a.chunks, a.kp, a.n_blocks, a.xcd_map, a.whole);
   } else {
-    hipLaunchKernelGGL((qmm_stream_multi_kernel<Tag, GS, MT, WV, BITS, SBPC, TSB>),
+    hipLaunchKernelGGL((qmm_stream_multi_kernel<Tag, GS, MT, WV, BITS, SBPC, TSB, RW>),
                        dim3(p.grid_x), dim3(64 * WV), lds, st, a, m);
   }
 }
 
 // The pair-streaming kernel when the plan allows it and every matrix has its
-// pair table (4-bit, gs 64 / 128, one activation block, 4 wavefronts).
+// pair table (4-bit, gs 64 / 128, one activation block; 4 wavefronts and
+// 64-row blocks, or 8 wavefronts and 128-row blocks).  The launcher has
+// already turned a 128-row plan into its 64-row equivalent when the tables
+// are missing.
 template <typename Tag, int GS, int MT, int WV, int BITS>
 static void launch_stream_t(const StreamPlan& p, hipStream_t st, const StreamArgs& a,
                             const StreamSegs& m) {
-  if constexpr (BITS == 4 && GS >= 64 && MT == 1 && WV == 4) {
-    if (p.tsb && segs_have_pairs(m)) {
-      launch_stream_k<Tag, GS, MT, WV, BITS, true>(p, st, a, m);
+  if constexpr (BITS == 4 && GS >= 64 && MT == 1) {
+    if (p.tsb && p.rw == 2 && WV == 8) {
+      launch_stream_k<Tag, GS, MT, 8, BITS, true, 2>(p, st, a, m);
+      return;
+    }
+    if (p.tsb && p.rw == 1 && WV == 4 && segs_have_pairs(m)) {
+      launch_stream_k<Tag, GS, MT, WV, BITS, true, 1>(p, st, a, m);
       return;
     }
   }
-  launch_stream_k<Tag, GS, MT, WV, BITS, false>(p, st, a, m);
+  launch_stream_k<Tag, GS, MT, WV, BITS, false, 1>(p, st, a, m);
 }
 
 template <typename Tag, int GS, int BITS>
@@ -589,11 +673,22 @@ static void allow_lds_t() {
   constexpr int SBPC = BITS == 8 && WV == 8 ? 8 : kSbPieces;
   constexpr int lds = Stream<Tag, GS, MT, WV, SBPC, BITS>::LDS_BYTES;
   (void)hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&qmm_stream_kernel<Tag, GS, MT, WV, BITS, SBPC, false>),
+      reinterpret_cast<const void*>(&qmm_stream_kernel<Tag, GS, MT, WV, BITS, SBPC, false, 1>),
       hipFuncAttributeMaxDynamicSharedMemorySize, lds);
   (void)hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&qmm_stream_multi_kernel<Tag, GS, MT, WV, BITS, SBPC, false>),
+      reinterpret_cast<const void*>(
+          &qmm_stream_multi_kernel<Tag, GS, MT, WV, BITS, SBPC, false, 1>),
       hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  if constexpr (BITS == 4 && GS >= 64 && MT == 1 && WV == 8) {
+    constexpr int lds2 = Stream<Tag, GS, MT, 8, kSbPieces, 4, 2, true>::LDS_BYTES;
+    (void)hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&qmm_stream_kernel<Tag, GS, 1, 8, 4, kSbPieces, true, 2>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, lds2);
+    (void)hipFuncSetAttribute(
+        reinterpret_cast<const void*>(
+            &qmm_stream_multi_kernel<Tag, GS, 1, 8, 4, kSbPieces, true, 2>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, lds2);
+  }
 }
 
 template <typename Tag, int GS>
@@ -688,12 +783,23 @@ static bool use_persist(int64_t M, int64_t K, int64_t N, int gs, int bits,
 
 // The streaming kernel over the matrices of m (their row blocks one grid of
 // n_cols / 64 blocks), after the caller's argument checks.
-static int launch_streaming(const void* x, int x_dtype, const StreamSegs& m, int64_t M, int64_t K,
-                            int64_t n_cols, int gs, int bits, const dfmi_qmm_tuning* tuning,
-                            void* workspace, size_t workspace_bytes, hipStream_t st) {
+static int launch_streaming(const void* x, int x_dtype, const StreamSegs& segs, int64_t M,
+                            int64_t K, int64_t n_cols, int gs, int bits,
+                            const dfmi_qmm_tuning* tuning, void* workspace,
+                            size_t workspace_bytes, hipStream_t st) {
   StreamPlan p;
-  const int rc = plan_stream(M, K, n_cols, gs, bits, tuning, p);
+  int64_t Ns[kMaxSeg];
+  for (int i = 0; i < segs.nseg; ++i) Ns[i] = segs.seg[i].N;
+  const int rc = plan_stream(M, K, n_cols, gs, bits, tuning, p, Ns, segs.nseg);
   if (rc != DFMI_OK) return rc;
+  if (p.rw == 2 && !segs_have_pairs(segs)) plan_as_rows64(p);
+  // each matrix's first block in the launch's block size
+  StreamSegs m = segs;
+  int blk = 0;
+  for (int i = 0; i < m.nseg; ++i) {
+    m.seg[i].blk0 = blk;
+    blk += (int)((Ns[i] + kStreamRows * p.rw - 1) / (kStreamRows * p.rw));
+  }
   StreamArgs a;
   a.x = static_cast<const uint16_t*>(x);
   a.partials = nullptr;
@@ -713,7 +819,7 @@ static int launch_streaming(const void* x, int x_dtype, const StreamSegs& m, int
   a.kp = p.kp;
   a.n_blocks = p.n_blocks;
   a.xcd_map = p.xcd_map;
-  a.pstride = kStreamRows * (p.n_blocks - p.whole);
+  a.pstride = kStreamRows * p.rw * (p.n_blocks - p.whole);
   a.whole = p.whole;
   allow_lds_all();
   if (x_dtype == DFMI_BF16) launch_stream<BF16>(gs, p, st, a, m);
@@ -772,9 +878,10 @@ extern "C" int dfmi_qmm_plan(int64_t M, int64_t K, const int64_t* Ns, int nseg, 
     if (cols <= 0) return DFMI_OK;
   }
   StreamPlan p;
-  const int rc = plan_stream(M, K, cols, group_size, bits, tuning, p);
+  const int rc = plan_stream(M, K, cols, group_size, bits, tuning, p, Ns, nseg);
   if (rc != DFMI_OK) return rc;
   out->streaming = 1;
+  out->rows_per_block = kStreamRows * p.rw;
   out->waves = p.WV;
   out->k_splits = p.kp;
   out->whole_blocks = p.whole;
@@ -977,7 +1084,8 @@ extern "C" size_t dfmi_qmm_multi_workspace_bytes(int64_t M, int64_t K, const int
   const int64_t cols = multi_stream_cols(M, K, Ns, nseg, group_size, bits);
   if (cols > 0) {
     StreamPlan p;
-    return plan_stream(M, K, cols, group_size, bits, nullptr, p) == DFMI_OK ? p.ws_bytes : 0;
+    return plan_stream(M, K, cols, group_size, bits, nullptr, p, Ns, nseg) == DFMI_OK ? p.ws_bytes
+                                                                                   : 0;
   }
   size_t ws = 0;
   for (int i = 0; i < nseg; ++i)

@@ -162,9 +162,11 @@ struct Stream {
   // weights with one activation block and 4 wavefronts likewise fit 80 KB in
   // two stages; with two blocks they would still need 96 KB (one workgroup
   // per CU), so they keep three.
-  // Two row groups (one workgroup per CU) take four stages.
+  // Two row groups take four stages with a scale window (160 KB, one
+  // workgroup per CU) and three with pair streaming (78 KB, two per CU).
   static constexpr int DEPTH =
-      RW == 2 ? 4 : ((MT == 2 && BITS == 4) || (MT == 1 && BITS == 8 && WV == 4) ? 2 : 3);
+      RW == 2 ? (TSB ? 3 : 4)
+              : ((MT == 2 && BITS == 4) || (MT == 1 && BITS == 8 && WV == 4) ? 2 : 3);
   // gs >= 64: a lane's two k-blocks take adjacent words (one 8-byte LDS read);
   // gs = 32: k-block j is group 2*wave + j, so the blocks stay group-pure.
   static constexpr bool PAIR = GS >= 64;

@@ -63,12 +63,17 @@ const char *dfmi_last_error(void);
  *         wavefronts (8 needs M <= 16 and K % 512 == 0);
  *   k_splits: streaming kernel, workgroups that split K of one output block
  *         (raised if a split's K range would exceed one scale / bias window
- *         of 120 groups). */
+ *         of 120 groups);
+ *   rows_per_block: streaming kernel, 64 or 128 weight rows per workgroup
+ *         (128: the pair-streaming plan of 4-bit gs 64 / 128 shapes with
+ *         M <= 16 and N a multiple of 128, waves_per_block 0; DFMI_EINVAL
+ *         otherwise); 0 automatic. */
 typedef struct dfmi_qmm_tuning {
   int path;
   int tiles_per_wave;
   int waves_per_block;
   int k_splits;
+  int rows_per_block;
 } dfmi_qmm_tuning;
 
 /*
@@ -137,7 +142,8 @@ int dfmi_sb_pairs(const void *scales, const void *biases, int dtype, int64_t N, 
  * fields are then 0).  blocks: 64-row blocks of the grid; whole_blocks: the
  * first blocks run unsplit, the rest are split k_splits ways; workgroups:
  * the grid; pair_streaming: the plan runs on the pair-streaming kernel when
- * pair tables are given. */
+ * pair tables are given; rows_per_block: 64 or 128 (a 128-row plan runs as
+ * its 64-row equivalent, same results, when the pair tables are missing). */
 typedef struct dfmi_qmm_plan_info {
   int streaming;
   int waves;
@@ -146,6 +152,7 @@ typedef struct dfmi_qmm_plan_info {
   int blocks;
   int workgroups;
   int pair_streaming;
+  int rows_per_block;
 } dfmi_qmm_plan_info;
 int dfmi_qmm_plan(int64_t M, int64_t K, const int64_t *Ns, int nseg, int group_size, int bits,
                   const dfmi_qmm_tuning *tuning, dfmi_qmm_plan_info *out);

@@ -147,8 +147,8 @@ def test_workspace_queries(lib):
 
 
 def _plan(lib, M, K, Ns, bits=4, gs=64, tuning=None):
-    """(waves, k_splits, whole_blocks, workgroups, pair_streaming) of the
-    streaming launch, and the workspace bytes the matching query reports."""
+    """(waves, k_splits, whole_blocks, workgroups, pair_streaming, rows_per_block)
+    of the streaming launch, checked against the workspace query."""
     from dflash_mlx_amd import _lib
     ns = (ctypes.c_int64 * len(Ns))(*Ns)
     info = _lib.QmmPlanInfo()
@@ -159,39 +159,55 @@ def _plan(lib, M, K, Ns, bits=4, gs=64, tuning=None):
         ws = lib.dfmi_qmm_workspace_bytes_ex(M, K, Ns[0], gs, bits, tptr)
     else:
         ws = lib.dfmi_qmm_multi_workspace_bytes(M, K, ns, len(Ns), gs, bits)
-    # counters + kp fp32 partials of the split blocks' 64 rows
-    split_rows = 64 * (info.blocks - info.whole_blocks)
+    # counters + kp fp32 partials of the split blocks' rows
+    split_rows = info.rows_per_block * (info.blocks - info.whole_blocks)
     assert ws == (65536 + info.k_splits * M * split_rows * 4 if info.k_splits > 1 else 0)
     assert info.workgroups == info.whole_blocks + (info.blocks - info.whole_blocks) * info.k_splits
-    return info.waves, info.k_splits, info.whole_blocks, info.workgroups, info.pair_streaming
+    return (info.waves, info.k_splits, info.whole_blocks, info.workgroups, info.pair_streaming,
+            info.rows_per_block)
 
 
 def test_streaming_split_plans(lib):
     """The streaming matmul's launch plans, read back through the plan query
     (and checked against the workspace query)."""
-    # M <= 16, 4-bit, gs 64: pair-streaming plans, 4 wavefronts, up to three
-    # workgroups per CU.  Fewer than 256 blocks: one workgroup per CU, two
-    # when a split would still stream >= 12 steps of 256 k.
-    assert _plan(lib, 16, 4096, [4096]) == (4, 4, 0, 256, 1)
-    assert _plan(lib, 16, 5120, [5120]) == (4, 3, 0, 240, 1)
-    assert _plan(lib, 16, 5120, [5120, 1024, 1024]) == (4, 2, 0, 224, 1)  # 27B q/k/v
-    assert _plan(lib, 16, 17408, [5120]) == (4, 6, 0, 480, 1)   # 68 steps: 2 per CU
-    assert _plan(lib, 16, 12288, [4096]) == (4, 8, 0, 512, 1)
-    assert _plan(lib, 8, 12288, [4096]) == (4, 8, 0, 512, 1)    # any M <= 16
+    # M <= 16, 4-bit, gs 64: pair-streaming plans.  Fewer than 256 blocks:
+    # K split so that one workgroup per CU runs (kp = 256 / blocks).  128-row
+    # blocks (8 wavefronts, two per CU) where every matrix is a multiple of
+    # 128 rows and a workgroup streams >= 8 steps on average, else 64-row
+    # blocks (4 wavefronts, three per CU).
+    assert _plan(lib, 16, 4096, [4096]) == (4, 4, 0, 256, 1, 64)
+    assert _plan(lib, 16, 5120, [5120]) == (4, 3, 0, 240, 1, 64)
+    assert _plan(lib, 16, 5120, [5120, 1024, 1024]) == (4, 2, 0, 224, 1, 64)  # 27B q/k/v
+    assert _plan(lib, 16, 17408, [5120]) == (8, 6, 0, 240, 1, 128)      # 27B down
+    assert _plan(lib, 8, 12288, [4096]) == (4, 4, 0, 256, 1, 64)        # any M <= 16
+    assert _plan(lib, 16, 4096, [12288, 12288]) == (8, 1, 0, 192, 1, 128)  # 9B gate/up
     # a split's K range stays within one scale window (120 groups): 68 steps
     # of 4 groups need at least 3 splits, whatever the grid
     assert _plan(lib, 16, 17408, [40960])[1:3] == (3, 0)
-    # 256..511 blocks: whole; 512..767: two whole blocks per CU, the rest one
-    # piece per CU; >= 768: whole rounds, the last partial round split
-    assert _plan(lib, 16, 4096, [12288, 12288]) == (4, 1, 0, 384, 1)   # 9B gate/up
-    assert _plan(lib, 16, 5120, [32768]) == (4, 1, 0, 512, 1)
-    assert _plan(lib, 16, 5120, [17408, 17408]) == (4, 8, 512, 512 + 32 * 8, 1)  # 27B gate/up
-    assert _plan(lib, 16, 5120, [40960]) == (4, 2, 512, 512 + 128 * 2, 1)
-    assert _plan(lib, 16, 5120, [518 * 64 - 51]) == (4, 20, 512, 512 + 6 * 20, 1)
-    assert _plan(lib, 16, 5120, [151936]) == (4, 11, 2304, 2304 + 70 * 11, 1)  # lm_head rows
+    # 256..511 blocks of 128 rows: one whole block per CU and the rest split
+    # into one piece per CU; 512..767 blocks of 64 rows: two whole per CU and
+    # one piece; whole rounds beyond
+    assert _plan(lib, 16, 5120, [32768]) == (8, 1, 0, 256, 1, 128)
+    assert _plan(lib, 16, 5120, [17408, 17408]) == (8, 16, 256, 256 + 16 * 16, 1, 128)  # 27B gate/up
+    assert _plan(lib, 16, 5120, [40960]) == (8, 4, 256, 256 + 64 * 4, 1, 128)
+    assert _plan(lib, 16, 5120, [151936]) == (8, 1, 0, 1187, 1, 128)   # lm_head rows
+    # N not a multiple of 128: 64-row blocks
+    assert _plan(lib, 16, 5120, [518 * 64 - 51]) == (4, 20, 512, 512 + 6 * 20, 1, 64)
+    assert _plan(lib, 16, 5120, [5120, 1000]) == (4, 2, 0, 2 * 96, 1, 64)
+    # the 64-row plans on request
+    r64 = _lib_tuning(0, 0, 0, 0, 64)
+    assert _plan(lib, 16, 17408, [5120], tuning=r64) == (4, 3, 0, 240, 1, 64)
+    assert _plan(lib, 16, 5120, [34816], tuning=r64) == (4, 8, 512, 512 + 32 * 8, 1, 64)
+    assert _plan(lib, 16, 5120, [40960], tuning=r64) == (4, 2, 512, 512 + 128 * 2, 1, 64)
+    assert _plan(lib, 16, 5120, [5120], tuning=_lib_tuning(0, 0, 0, 5, 64)) == \
+        (4, 5, 0, 400, 1, 64)
+    # 128-row blocks with explicit splits
+    assert _plan(lib, 16, 5120, [5120], tuning=_lib_tuning(0, 0, 0, 3, 128)) == \
+        (8, 3, 0, 120, 1, 128)
     # gs 128 too; gs 32 and 8-bit weights keep the window plans
-    assert _plan(lib, 16, 5120, [5120], gs=128)[4] == 1
-    assert _plan(lib, 16, 5120, [5120], gs=32)[4] == 0
+    assert _plan(lib, 16, 5120, [17408, 17408], gs=128)[4:] == (1, 128)
+    assert _plan(lib, 16, 5120, [5120], gs=128)[4:] == (1, 64)
+    assert _plan(lib, 16, 5120, [5120], gs=32)[4:] == (0, 64)
     # M = 17..32, 4-bit: two activation blocks, two workgroups per CU,
     # splits toward 512 workgroups while each keeps >= 8 steps of 256 k;
     # whole rounds of 512 then a split tail
@@ -204,12 +220,19 @@ def test_streaming_split_plans(lib):
     assert _plan(lib, 16, 4096, [4096], bits=8)[:2] == (8, 4)
     # explicit splits / wavefronts take the window planner; the plan still
     # runs on the pair kernel when it has 4 wavefronts and one activation block
-    t = _lib_tuning(0, 0, 4, 2)
-    assert _plan(lib, 16, 5120, [5120], tuning=t) == (4, 2, 0, 160, 1)
-    t = _lib_tuning(0, 0, 8, 2)
-    assert _plan(lib, 16, 5120, [5120], tuning=t) == (8, 2, 0, 160, 0)
-
-
-def _lib_tuning(path, tiles, waves, splits):
+    assert _plan(lib, 16, 5120, [5120], tuning=_lib_tuning(0, 0, 4, 2)) == (4, 2, 0, 160, 1, 64)
+    assert _plan(lib, 16, 5120, [5120], tuning=_lib_tuning(0, 0, 8, 2)) == (8, 2, 0, 160, 0, 64)
+    # 128-row blocks need a pair-streaming shape with N a multiple of 128
     from dflash_mlx_amd import _lib
-    return _lib.QmmTuning(path, tiles, waves, splits)
+    for (M, K, N, gs, bits) in ((16, 5120, 5000, 64, 4), (32, 5120, 5120, 64, 4),
+                                (16, 5120, 5120, 32, 4), (16, 5120, 5120, 64, 8)):
+        ns = (ctypes.c_int64 * 1)(N)
+        info = _lib.QmmPlanInfo()
+        t = _lib_tuning(0, 0, 0, 0, 128)
+        assert lib.dfmi_qmm_plan(M, K, ns, 1, gs, bits, ctypes.byref(t), ctypes.byref(info)) == \
+            _lib.DFMI_EINVAL
+
+
+def _lib_tuning(path, tiles, waves, splits, rows=0):
+    from dflash_mlx_amd import _lib
+    return _lib.QmmTuning(path, tiles, waves, splits, rows)

@@ -133,6 +133,28 @@ def test_pairs_bit_identical_forced_splits(dev, kp):
     assert np.array_equal(from_dev(y0, "bf16"), from_dev(y1, "bf16"))
 
 
+@pytest.mark.parametrize("N,K,kp", [(5120, 5120, 3), (5120, 17408, 6), (7168, 5120, 2),
+                                    (34816, 2048, 1), (1024, 4096, 8)])
+def test_rows128_matches_rows64(dev, N, K, kp):
+    """128-row blocks (two row groups of 4 wavefronts sharing the activation
+    stage) give the same sums as 64-row blocks under the same K splits:
+    bit-identical with the table, and without it (the 64-row equivalent the
+    launcher runs)."""
+    L = _lib()
+    M, gs = 16, 64
+    _, (xt, wt, st, bt) = _case(dev, M, K, N, gs, "bf16", seed=N + K + kp)
+    pt = _pairs(st, bt)
+    t128 = L.QmmTuning(0, 0, 0, kp, 128)
+    t64 = L.QmmTuning(0, 0, 0, kp, 64)
+    i128, i64 = _plan(M, K, [N], gs, t128), _plan(M, K, [N], gs, t64)
+    assert (i128.rows_per_block, i128.waves, i128.k_splits) == (128, 8, kp)
+    assert (i64.rows_per_block, i64.waves, i64.k_splits) == (64, 4, kp)
+    ys = [from_dev(_launch(dev, xt, wt, st, bt, p, N, gs, t), "bf16")
+          for (p, t) in ((pt, t128), (None, t128), (pt, t64), (None, t64))]
+    for y in ys[1:]:
+        assert np.array_equal(ys[0], y)
+
+
 def test_pairs_closed_form_exact(dev):
     # dyadic scales / biases, +-1 activations: every product and sum is exact
     # in fp32, so the table path must reproduce the oracle bit for bit on a
