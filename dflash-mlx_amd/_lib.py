@@ -98,6 +98,11 @@ _SIGNATURES = {
                                          _int, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                          _c_void_p, _size, _c_void_p]),
     "dfmi_lmhead_workspace_bytes": (_size, [_i64]),
+    "dfmi_lmhead_greedy_accept_pairs": (_int, [_c_void_p, _int, _c_void_p, _c_void_p, _c_void_p,
+                                               _c_void_p, _c_void_p, _float, _c_void_p, _i64,
+                                               _i64, _i64, _int, _int, _c_void_p, _c_void_p,
+                                               _c_void_p, _c_void_p, _c_void_p, _size,
+                                               _c_void_p]),
     "dfmi_match_acceptance_length": (_int, [_c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p]),
     "dfmi_gated_delta_tape": (_int, [_c_void_p] * 10 + [_i64] * 6 + [_int] * 5 + [_c_void_p]),
     "dfmi_tape_replay": (_int, [_c_void_p] * 6 + [_i64] * 6 + [_int] * 4 + [_c_void_p]),

@@ -118,6 +118,7 @@ struct LmArgs {
   const uint32_t* w;
   const uint16_t* s;
   const uint16_t* b;
+  const uint32_t* t;  // [K/gs][V] (scale, bias) pairs (pair-streaming kernel) or null
   const uint8_t* mask;
   uint16_t* logits;  // [M, V] or null
   float softcap;
@@ -184,9 +185,11 @@ __global__ __launch_bounds__(kMaxWaves * 64) void lmhead_greedy_kernel(LmArgs a)
   greedy_publish_and_finish(a.out, s_best, 0, a.M, (unsigned)a.n_blocks, &s_g);
 }
 
-template <typename Tag, int GS, int MT, int WV>
+// TSB / RW: the pair-streaming main loop with 128-row blocks (two row groups
+// of 4 wavefronts sharing the activation stage); the window loop otherwise.
+template <typename Tag, int GS, int MT, int WV, bool TSB = false, int RW = 1>
 __global__ __launch_bounds__(64 * WV) void lmhead_stream_kernel(LmArgs a) {
-  using S = Stream<Tag, GS, MT, WV>;
+  using S = Stream<Tag, GS, MT, WV, kSbPieces, 4, RW, TSB>;
   constexpr int kThreads = 64 * WV;
   // Dynamic LDS only (two workgroups of 4 wavefronts fill a CU's LDS): the
   // epilogue's argmax keys and greedy scratch follow the reduction buffer.
@@ -201,6 +204,7 @@ __global__ __launch_bounds__(64 * WV) void lmhead_stream_kernel(LmArgs a) {
   cx.w = buffer_rsrc(a.w, (uint32_t)a.V * (uint32_t)(a.K / 2));
   cx.s = buffer_rsrc(a.s, (uint32_t)a.V * (uint32_t)(a.K / GS) * 2u);
   cx.b = buffer_rsrc(a.b, (uint32_t)a.V * (uint32_t)(a.K / GS) * 2u);
+  if constexpr (TSB) cx.t = buffer_rsrc(a.t, (uint32_t)a.V * (uint32_t)(a.K / GS) * 4u);
   cx.K = a.K;
   cx.M = a.M;
   cx.N = a.V;
@@ -216,8 +220,9 @@ __global__ __launch_bounds__(64 * WV) void lmhead_stream_kernel(LmArgs a) {
     for (int mt = 0; mt < MT; ++mt) acc[t][mt] = zero4();
   S::run(cx, 0, a.K / S::CK, acc);
 
-  // sum the WV wavefronts' partial tiles through LDS (the stages are free:
-  // every DMA has landed and every wavefront is past its last LDS read)
+  // sum the partial tiles of each row group's KW wavefronts through LDS (the
+  // stages are free: every DMA has landed and every wavefront is past its
+  // last LDS read), in k-slice order
   __syncthreads();
   float* red = reinterpret_cast<float*>(dfmi_smem);
   {
@@ -233,19 +238,42 @@ __global__ __launch_bounds__(64 * WV) void lmhead_stream_kernel(LmArgs a) {
   __syncthreads();
   const float capr = a.softcap > 0.f ? round_t<Tag>(a.softcap) : 0.f;
   const float neg = round_t<Tag>(-1e9f);
-  for (int e = tid; e < S::RED_FLOATS; e += kThreads) {
-    float sum = red[e];
+  // Every element a thread visits has its row m = 16 mt + 4 (lane >> 4) + j
+  // with j = wave & 3 (kThreads is a multiple of 256): the thread keeps one
+  // best key per activation block, the 16 lanes of a row group combine
+  // theirs, and one lane per row updates the workgroup's key in LDS.
+  constexpr int PER = RW * S::RED_FLOATS / kThreads;
+  unsigned long long best[MT];
 #pragma unroll
-    for (int wv = 1; wv < WV; ++wv) sum += red[wv * S::RED_FLOATS + e];
-    const int l = e & 63, j = (e >> 6) & 3, tm = e >> 8;
-    const int n = cx.n0 + (tm / MT) * 16 + (l & 15);
+  for (int u = 0; u < MT; ++u) best[u] = 0ull;
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    const int e = q * kThreads + tid;
+    const int rg = e / S::RED_FLOATS, eo = e % S::RED_FLOATS;
+    const float* rr = red + rg * S::KW * S::RED_FLOATS + eo;
+    float sum = rr[0];
+#pragma unroll
+    for (int k = 1; k < S::KW; ++k) sum += rr[k * S::RED_FLOATS];
+    const int l = eo & 63, j = (eo >> 6) & 3, tm = eo >> 8;
+    const int n = cx.n0 + kStreamRows * rg + (tm / MT) * 16 + (l & 15);
     const int m = (tm % MT) * 16 + 4 * (l >> 4) + j;
     if (m < a.M && n < a.V) {
       float v = logit_value<Tag>(sum, capr);
       if (a.logits) a.logits[(int64_t)m * a.V + n] = Num<Tag>::f2h(v);
       if (a.mask && a.mask[n]) v = neg;
-      atomicMax(&s_best[m], argmax_key(v, (uint32_t)n));
+      const unsigned long long key = argmax_key(v, (uint32_t)n);
+#pragma unroll
+      for (int u = 0; u < MT; ++u)
+        if (u == tm % MT) best[u] = umax64(best[u], key);
     }
+  }
+#pragma unroll
+  for (int u = 0; u < MT; ++u) {
+    unsigned long long k = best[u];
+#pragma unroll
+    for (int d = 1; d < 16; d <<= 1) k = umax64(k, __shfl_xor(k, d, 64));
+    const int m = 16 * u + 4 * (cx.lane >> 4) + (cx.wave & 3);
+    if ((cx.lane & 15) == 0 && m < a.M && k != 0ull) atomicMax(&s_best[m], k);
   }
   __syncthreads();
   greedy_publish_and_finish(a.out, s_best, 0, a.M, (unsigned)a.n_blocks, s_g);
@@ -345,16 +373,24 @@ static void launch_lm_tag(int gs, int mt, bool kfull, int blocks, int waves, hip
   }
 }
 
-template <typename Tag, int GS, int MT, int WV>
+template <typename Tag, int GS, int MT, int WV, bool TSB = false, int RW = 1>
 static void launch_lm_stream_t(int blocks, hipStream_t st, const LmArgs& a) {
-  constexpr int lds = Stream<Tag, GS, MT, WV>::LDS_BYTES;
+  constexpr int lds = Stream<Tag, GS, MT, WV, kSbPieces, 4, RW, TSB>::LDS_BYTES;
   // dynamic LDS above 64 KiB needs the kernel attribute raised (once)
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&lmhead_stream_kernel<Tag, GS, MT, WV>),
+      reinterpret_cast<const void*>(&lmhead_stream_kernel<Tag, GS, MT, WV, TSB, RW>),
       hipFuncAttributeMaxDynamicSharedMemorySize, lds);
   (void)attr;
-  hipLaunchKernelGGL((lmhead_stream_kernel<Tag, GS, MT, WV>), dim3(blocks), dim3(64 * WV), lds,
-                     st, a);
+  hipLaunchKernelGGL((lmhead_stream_kernel<Tag, GS, MT, WV, TSB, RW>), dim3(blocks),
+                     dim3(64 * WV), lds, st, a);
+}
+
+// With the pair table (gs 64 / 128, one activation block): 128-row blocks,
+// 8 wavefronts in two row groups, two workgroups per CU.
+template <typename Tag>
+static void launch_lm_pairs(int gs, int blocks, hipStream_t st, const LmArgs& a) {
+  if (gs == 64) launch_lm_stream_t<Tag, 64, 1, 8, true, 2>(blocks, st, a);
+  else launch_lm_stream_t<Tag, 128, 1, 8, true, 2>(blocks, st, a);
 }
 
 // 4 wavefronts (two workgroups per CU): the vocabulary gives thousands of
@@ -412,13 +448,12 @@ extern "C" int dfmi_greedy_accept(const void* logits, int logits_dtype, const ui
   return check_launch("dfmi_greedy_accept");
 }
 
-extern "C" int dfmi_lmhead_greedy_accept(const void* h, int h_dtype, const uint32_t* w_q,
-                                         const void* scales, const void* biases,
-                                         const uint8_t* suppress_mask, float softcap,
-                                         const uint32_t* verify_ids, int64_t M, int64_t K,
-                                         int64_t V, int group_size, int bits, uint32_t* posterior,
-                                         int32_t* accept_len, uint32_t* bonus, void* logits_out,
-                                         void* workspace, size_t workspace_bytes, void* stream) {
+extern "C" int dfmi_lmhead_greedy_accept_pairs(
+    const void* h, int h_dtype, const uint32_t* w_q, const void* scales, const void* biases,
+    const uint32_t* sb_pairs, const uint8_t* suppress_mask, float softcap,
+    const uint32_t* verify_ids, int64_t M, int64_t K, int64_t V, int group_size, int bits,
+    uint32_t* posterior, int32_t* accept_len, uint32_t* bonus, void* logits_out, void* workspace,
+    size_t workspace_bytes, void* stream) {
   if (h_dtype != DFMI_BF16 && h_dtype != DFMI_F16) {
     set_error("dfmi_lmhead_greedy_accept: dtype %d unsupported (bf16 or f16)", h_dtype);
     return DFMI_EINVAL;
@@ -437,8 +472,10 @@ extern "C" int dfmi_lmhead_greedy_accept(const void* h, int h_dtype, const uint3
     set_error("dfmi_lmhead_greedy_accept: null pointer");
     return DFMI_EINVAL;
   }
-  if (!aligned16(h) || !aligned16(w_q) || !aligned16(scales) || !aligned16(biases)) {
-    set_error("dfmi_lmhead_greedy_accept: h, w_q, scales and biases must be 16-byte aligned");
+  if (!aligned16(h) || !aligned16(w_q) || !aligned16(scales) || !aligned16(biases) ||
+      (sb_pairs && !aligned16(sb_pairs))) {
+    set_error("dfmi_lmhead_greedy_accept: h, w_q, scales, biases and sb_pairs must be 16-byte "
+              "aligned");
     return DFMI_EINVAL;
   }
   LmArgs a;
@@ -448,6 +485,7 @@ extern "C" int dfmi_lmhead_greedy_accept(const void* h, int h_dtype, const uint3
   a.w = w_q;
   a.s = static_cast<const uint16_t*>(scales);
   a.b = static_cast<const uint16_t*>(biases);
+  a.t = sb_pairs;
   a.mask = suppress_mask;
   a.logits = static_cast<uint16_t*>(logits_out);
   a.softcap = softcap;
@@ -460,6 +498,14 @@ extern "C" int dfmi_lmhead_greedy_accept(const void* h, int h_dtype, const uint3
   const bool kfull = (K % kChunkK) == 0;
   const int mt = M <= 16 ? 1 : 2;
   hipStream_t st = static_cast<hipStream_t>(stream);
+  // with the pair table: the pair-streaming loop, 128 vocabulary rows per
+  // workgroup (the same logits, summed in the same order, as the window loop)
+  if (sb_pairs && M <= 16 && group_size >= 64 && stream_eligible(M, K, V, group_size)) {
+    a.n_blocks = (int)((V + 2 * kStreamRows - 1) / (2 * kStreamRows));
+    if (h_dtype == DFMI_BF16) launch_lm_pairs<BF16>(group_size, a.n_blocks, st, a);
+    else launch_lm_pairs<F16>(group_size, a.n_blocks, st, a);
+    return check_launch("dfmi_lmhead_greedy_accept");
+  }
   // the streaming loop takes the whole K range in one scale / bias window
   if (stream_eligible(M, K, V, group_size) && K / group_size <= sb_max_groups(kSbPieces)) {
     if (h_dtype == DFMI_BF16) launch_lm_stream<BF16>(group_size, mt, a.n_blocks, st, a);
@@ -470,6 +516,19 @@ extern "C" int dfmi_lmhead_greedy_accept(const void* h, int h_dtype, const uint3
   if (h_dtype == DFMI_BF16) launch_lm_tag<BF16>(group_size, mt, kfull, a.n_blocks, waves, st, a);
   else launch_lm_tag<F16>(group_size, mt, kfull, a.n_blocks, waves, st, a);
   return check_launch("dfmi_lmhead_greedy_accept");
+}
+
+extern "C" int dfmi_lmhead_greedy_accept(const void* h, int h_dtype, const uint32_t* w_q,
+                                         const void* scales, const void* biases,
+                                         const uint8_t* suppress_mask, float softcap,
+                                         const uint32_t* verify_ids, int64_t M, int64_t K,
+                                         int64_t V, int group_size, int bits, uint32_t* posterior,
+                                         int32_t* accept_len, uint32_t* bonus, void* logits_out,
+                                         void* workspace, size_t workspace_bytes, void* stream) {
+  return dfmi_lmhead_greedy_accept_pairs(h, h_dtype, w_q, scales, biases, nullptr, suppress_mask,
+                                         softcap, verify_ids, M, K, V, group_size, bits,
+                                         posterior, accept_len, bonus, logits_out, workspace,
+                                         workspace_bytes, stream);
 }
 
 extern "C" int dfmi_match_acceptance_length(const uint32_t* drafted, const uint32_t* posterior,

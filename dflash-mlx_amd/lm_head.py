@@ -52,9 +52,13 @@ def lm_head_greedy_accept(h: torch.Tensor, w: torch.Tensor, scales: torch.Tensor
                           biases: torch.Tensor, *, verify_ids: Optional[torch.Tensor] = None,
                           suppress_token_mask: Optional[torch.Tensor] = None,
                           softcap: Optional[float] = None, group_size: int = 64, bits: int = 4,
-                          return_logits: bool = False) -> GreedyAcceptResult:
+                          return_logits: bool = False,
+                          pairs: Optional[torch.Tensor] = None) -> GreedyAcceptResult:
     """Fused int4 lm_head + greedy argmax + accept/bonus for ``h [..., K]``
-    with at most 32 verify rows."""
+    with at most 32 verify rows.  ``pairs``: the lm_head's pair table
+    (``_runtime.build_sb_pairs``); when None, the one cached for ``scales``
+    is used where the pair-streaming loop applies.  Outputs do not depend
+    on it."""
     for t, name in ((h, "h"), (w, "w"), (scales, "scales"), (biases, "biases")):
         _runtime.require_device(t, name)
     lib = _lib.load()
@@ -75,9 +79,11 @@ def lm_head_greedy_accept(h: torch.Tensor, w: torch.Tensor, scales: torch.Tensor
     bonus = torch.empty((1,), dtype=torch.int32, device=dev) if ids is not None else None
     logits = torch.empty((M, V), dtype=h.dtype, device=dev) if return_logits else None
     ws, ws_bytes = _runtime.workspace(dev, int(lib.dfmi_lmhead_workspace_bytes(M)), "greedy")
-    status = lib.dfmi_lmhead_greedy_accept(
+    if pairs is None and _runtime.pair_shape(M, K, V, group_size, bits):
+        pairs = _runtime.PAIRS.get(s, b)
+    status = lib.dfmi_lmhead_greedy_accept_pairs(
         h2.data_ptr(), _runtime.dtype_code(h2.dtype), wq.data_ptr(), s.data_ptr(), b.data_ptr(),
-        mask_ptr, float(softcap) if softcap else 0.0, ids.data_ptr() if ids is not None else 0,
+        pairs.data_ptr() if pairs is not None else 0, mask_ptr, float(softcap) if softcap else 0.0, ids.data_ptr() if ids is not None else 0,
         M, K, V, int(group_size), int(bits), posterior.data_ptr(),
         accept.data_ptr() if accept is not None else 0,
         bonus.data_ptr() if bonus is not None else 0,

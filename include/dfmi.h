@@ -306,6 +306,21 @@ int dfmi_lmhead_greedy_accept(const void *h, int h_dtype, const uint32_t *w_q, c
                               uint32_t *bonus, void *logits_out, void *workspace,
                               size_t workspace_bytes, void *stream);
 size_t dfmi_lmhead_workspace_bytes(int64_t M);
+/*
+ * dfmi_lmhead_greedy_accept with the lm_head's pair table (sb_pairs
+ * [K/group_size][V], see dfmi_sb_pairs; 16-byte aligned; may be NULL): with
+ * it, M <= 16 and gs 64 / 128 sweep the vocabulary in 128-row blocks on the
+ * pair-streaming loop.  Same call sites replaced; identical outputs (the
+ * same logits, summed in the same order).
+ */
+int dfmi_lmhead_greedy_accept_pairs(const void *h, int h_dtype, const uint32_t *w_q,
+                                    const void *scales, const void *biases,
+                                    const uint32_t *sb_pairs, const uint8_t *suppress_mask,
+                                    float softcap, const uint32_t *verify_ids, int64_t M,
+                                    int64_t K, int64_t V, int group_size, int bits,
+                                    uint32_t *posterior, int32_t *accept_len, uint32_t *bonus,
+                                    void *logits_out, void *workspace, size_t workspace_bytes,
+                                    void *stream);
 
 /*
  * Gated-delta recurrence recording the innovation tape, over T steps

@@ -239,3 +239,54 @@ def test_functional_cache_and_module_tables(dev):
                                    ref)
     assert rel <= 1e-2
     assert not torch.equal(y0, y1)
+
+
+def _lmhead(dev, ht, wt, st, bt, pt, ids, M, K, V, gs):
+    """One dfmi_lmhead_greedy_accept_pairs call with logits out."""
+    import torch
+
+    from dflash_mlx_amd import _runtime
+
+    L = _lib()
+    lib = L.load()
+    post = torch.full((M,), -1, dtype=torch.int32, device=dev)
+    acc = torch.full((1,), -1, dtype=torch.int32, device=dev)
+    bonus = torch.full((1,), -1, dtype=torch.int32, device=dev)
+    logits = torch.full((M, V), float("nan"), dtype=ht.dtype, device=dev)
+    ws, wsb = _runtime.workspace(dev, int(lib.dfmi_lmhead_workspace_bytes(M)), "greedy")
+    rc = lib.dfmi_lmhead_greedy_accept_pairs(
+        ht.data_ptr(), _runtime.dtype_code(ht.dtype), wt.data_ptr(), st.data_ptr(), bt.data_ptr(),
+        pt.data_ptr() if pt is not None else 0, 0, 0.0, ids.data_ptr(), M, K, V, gs, 4,
+        post.data_ptr(), acc.data_ptr(), bonus.data_ptr(), logits.data_ptr(), ws, wsb,
+        _runtime.stream_ptr(dev))
+    L.check(rc, "dfmi_lmhead_greedy_accept_pairs")
+    torch.cuda.synchronize()
+    return post.cpu().numpy(), int(acc.item()), int(bonus.item()), logits
+
+
+@pytest.mark.parametrize("M,K,V,gs", [(16, 5120, 20000, 64), (15, 2048, 32000, 128),
+                                      (16, 4096, 40000, 64), (1, 1024, 1000, 64)])
+def test_lmhead_pairs_identical(dev, M, K, V, gs):
+    """The lm_head's pair-streaming sweep (128 vocabulary rows per
+    workgroup) gives the window loop's logits bit for bit, hence the same
+    tokens, accept length and bonus."""
+    import torch
+
+    host, (ht, wt, st, bt) = _case(dev, M, K, V, gs, "bf16", seed=V + M)
+    pt = _pairs(st, bt)
+    r0 = _lmhead(dev, ht, wt, st, bt, None, torch.zeros(M, dtype=torch.int32, device=dev),
+                 M, K, V, gs)
+    # verify ids that accept part of the block: the window loop's own tokens
+    ids = torch.tensor(np.concatenate([[0], r0[0][:M - 1]]).astype(np.int32), device=dev)
+    if M > 4:
+        ids[4] = (ids[4] + 1) % V  # break the chain after three accepted tokens
+    r0 = _lmhead(dev, ht, wt, st, bt, None, ids, M, K, V, gs)
+    r1 = _lmhead(dev, ht, wt, st, bt, pt, ids, M, K, V, gs)
+    assert np.array_equal(r0[0], r1[0]) and r0[1:3] == r1[1:3]
+    assert torch.equal(r0[3].view(torch.int16), r1[3].view(torch.int16))
+    if M > 4:
+        assert r1[1] == 3
+    # and the oracle's greedy on the kernel's own logits
+    lg = from_dev(r1[3], "bf16")
+    want = oracle.greedy_tokens_with_mask(lg, None, dtype="bf16")
+    assert np.array_equal(np.asarray(want).reshape(-1), r1[0].reshape(-1))
