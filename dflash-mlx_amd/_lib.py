@@ -88,6 +88,18 @@ _SIGNATURES = {
     "dfmi_gather_qmm_swiglu": (_int, [_c_void_p, _int, _i64, _c_void_p, _c_void_p, _c_void_p,
                                       _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                       _c_void_p, _i64, _i64, _i64, _i64, _int, _int, _c_void_p]),
+    "dfmi_gather_qmm_affine_pairs": (_int, [_c_void_p, _int, _i64, _c_void_p, _c_void_p,
+                                            _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                            _c_void_p, _i64, _i64, _i64, _i64, _int, _int,
+                                            _c_void_p, _size, _c_void_p]),
+    "dfmi_gather_qmm_swiglu_pairs": (_int, [_c_void_p, _int, _i64, _c_void_p, _c_void_p,
+                                            _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                            _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64,
+                                            _i64, _i64, _i64, _int, _int, _c_void_p, _size,
+                                            _c_void_p]),
+    "dfmi_gather_workspace_bytes": (_size, []),
+    "dfmi_moe_pairs": (_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _int, _i64, _i64,
+                              _i64, _c_void_p, _c_void_p]),
     "dfmi_moe_combine": (_int, [_c_void_p, _int, _c_void_p, _c_void_p, _c_void_p, _i64, _i64,
                                 _i64, _c_void_p]),
     "dfmi_greedy_accept": (_int, [_c_void_p, _int, _c_void_p, _c_void_p, _i64, _i64, _c_void_p,

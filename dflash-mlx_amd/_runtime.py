@@ -8,6 +8,7 @@ from __future__ import annotations
 
 import threading
 import weakref
+from typing import Optional, Tuple
 
 import torch
 
@@ -124,36 +125,70 @@ def build_sb_pairs(scales: torch.Tensor, biases: torch.Tensor) -> torch.Tensor:
     return pairs
 
 
+def moe_pair_shape(K: int, N: int, group_size: int, bits: int, swiglu: bool) -> bool:
+    """Expert shapes the pair-streaming gather takes (``dfmi_gather_qmm_*_pairs``):
+    4-bit, gs 64 / 128, whole 256-k steps, N a multiple of 64 (SwiGLU) or 128
+    (mirrors the library's rule; the pair count is checked per call)."""
+    return (int(bits) == 4 and int(group_size) in (64, 128) and int(K) >= 256
+            and int(K) % 256 == 0 and int(N) > 0 and int(N) % (64 if swiglu else 128) == 0)
+
+
+def build_moe_pairs(scales: torch.Tensor, biases: torch.Tensor,
+                    up_scales: Optional[torch.Tensor] = None,
+                    up_biases: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The ``[E][K/gs][N]`` (or SwiGLU-interleaved ``[E][K/gs][2N]``) uint32
+    pair table of routed experts (``dfmi_moe_pairs``), on the current stream."""
+    E, N, G = (int(d) for d in scales.shape)
+    cols = 2 * N if up_scales is not None else N
+    pairs = torch.empty((E, G, cols), dtype=torch.int32, device=scales.device)
+    lib = _lib.load()
+    status = lib.dfmi_moe_pairs(scales.data_ptr(), biases.data_ptr(),
+                                up_scales.data_ptr() if up_scales is not None else None,
+                                up_biases.data_ptr() if up_biases is not None else None,
+                                dtype_code(scales.dtype), E, N, G, pairs.data_ptr(),
+                                stream_ptr(scales.device))
+    _lib.check(status, "dfmi_moe_pairs")
+    return pairs
+
+
 class _PairCache:
     """Pair tables of the (scales, biases) tensors the functional operators
-    see, built on first use and kept while the scales tensor lives.  An entry
-    is valid only for the same two tensor objects at the same versions (an
-    in-place update rebuilds it).  Nothing is built during graph capture: the
-    caller then runs without a table (same plan, bit-identical result)."""
+    see, built on first use and kept while the tensors live.  An entry is
+    valid only for the same tensor objects at the same versions (an in-place
+    update rebuilds it).  Nothing is built during graph capture: the caller
+    then runs without a table (dense matmuls: the same plan, bit-identical
+    result; gathers: the plain gather's main loop).  ``experts`` selects the
+    routed-expert layout (``dfmi_moe_pairs``; with ``up`` the SwiGLU
+    interleave of two sets)."""
 
     def __init__(self):
         self._lock = threading.Lock()
-        self._entries: dict[int, tuple] = {}
+        self._entries: dict[tuple, tuple] = {}
 
-    def _drop(self, key: int):
+    def _drop(self, key: tuple):
         with self._lock:
             self._entries.pop(key, None)
 
-    def get(self, scales: torch.Tensor, biases: torch.Tensor):
-        key = id(scales)
-        ver = (scales._version, biases._version)
+    def get(self, scales: torch.Tensor, biases: torch.Tensor,
+            up: Optional[Tuple[torch.Tensor, torch.Tensor]] = None, *, experts: bool = False):
+        tensors = (scales, biases) + (tuple(up) if up is not None else ())
+        key = (id(scales), id(up[0]) if up is not None else 0, bool(experts))
+        ver = tuple(t._version for t in tensors)
         with self._lock:
             ent = self._entries.get(key)
         if ent is not None:
-            sref, bref, ever, pairs = ent
-            if sref() is scales and bref() is biases and ever == ver:
+            refs, ever, pairs = ent
+            if ever == ver and all(r() is t for r, t in zip(refs, tensors)):
                 return pairs
         if torch.cuda.is_current_stream_capturing():
             return None
-        pairs = build_sb_pairs(scales, biases)
-        sref = weakref.ref(scales, lambda _r, k=key: self._drop(k))
+        if experts:
+            pairs = build_moe_pairs(scales, biases, *(up if up is not None else ()))
+        else:
+            pairs = build_sb_pairs(scales, biases)
+        refs = tuple(weakref.ref(t, lambda _r, k=key: self._drop(k)) for t in tensors)
         with self._lock:
-            self._entries[key] = (sref, weakref.ref(biases), ver, pairs)
+            self._entries[key] = (refs, ver, pairs)
         return pairs
 
 

@@ -34,6 +34,9 @@ struct GatherArgs {
   const uint16_t* b[2];
   const int32_t* lhs;    // NULL: row p for pair p
   const int32_t* rhs;
+  const uint32_t* t;     // (scale, bias) pair tables [E][K/GS][N or 2N] (moe_stream_kernel)
+  uint32_t* ws_counters;  // moe_stream_kernel tail split: counters (zero between calls), or NULL
+  float* ws_partials;     // and the pieces' fp32 partial tiles
   uint16_t* y;           // [P, N]
   int P, K, N, E;
   int chunks;
@@ -565,6 +568,429 @@ __global__ __launch_bounds__(512) void gather_persist_kernel(GatherArgs a) {
 #undef DFMI_PERSIST_STEP
 }
 
+// ---------------------------------------------------------------------------
+// Pair-streaming persistent gather (moe_stream_kernel): K % 256 == 0, gs 64 /
+// 128, P <= kMoeMaxPairs, N a multiple of the unit's output columns, and a
+// (scale, bias) pair table per expert (dfmi_moe_pairs).  Two workgroups of 8
+// wavefronts per CU (80 KB of LDS each) run the 128-row pair-streaming main
+// loop (Stream<..., RW = 2, TSB>: two row groups of 4 wavefronts, each
+// wavefront a 64-k slice of every 256-k step) over a sequence of work units;
+// a unit is (segment, block of 128 weight rows), a segment being consecutive
+// pairs of one expert, cut every 16 pairs.  As in gather_persist_kernel the
+// pipeline (three stages in flight) runs across unit boundaries, and the
+// segment table is built by every workgroup from the pair ids.
+//
+// Rows of a unit: the matmul's rows n0 .. n0 + 127 of the expert, or for the
+// fused SwiGLU 64 output columns n0 .. n0 + 63 laid out per row group rg as
+// 32 gate rows (tiles 0, 1) then the same 32 up rows (tiles 2, 3), columns
+// n0 + 32 rg ..; the SwiGLU table interleaves the two pair tables the same
+// way ([E][K/gs][2N], 32 gate columns then 32 up columns per 64), so a
+// block's pairs are 128 consecutive table columns.
+//
+// Epilogue without a reduction pass: tile T of a row group is finished by
+// one of its wavefronts (wavefront T, or T % 2 for the SwiGLU so that gate
+// and up meet in one lane); the other three wavefronts leave their partial
+// tile in the stage freed by the fragment reads (24 KB), and the finishing
+// wavefront adds them to its own in a fixed order and stores.
+//
+// Units are dealt CU-major: with G = 2H workgroups, workgroup b takes units
+// (b % H) + H (2 i + b / H), so the two workgroups that share a CU under the
+// dispatcher's round-robin placement split one run of consecutive units.
+constexpr int kMoeMaxPairs = 256;
+constexpr int kMoeGroups = 512;  // two workgroups per CU
+// workspace of the tail split: counters of at most 255 tail units (4 KB),
+// then at most 256 pieces x 2 row groups x 4 tiles x 4 x 64 fp32 partials
+constexpr size_t kMoeWsCounterBytes = 4096;
+constexpr size_t kMoeWsBytes = kMoeWsCounterBytes + (size_t)(kMoeGroups / 2) * 2 * 1024 * 4;
+
+template <typename Tag, int GS>
+struct MoeLayout {
+  using S = Stream<Tag, GS, 1, 8, 4, 4, 2, true>;
+  static_assert(S::DEPTH == kPersistStages && S::NB == 128 && S::CK == 256, "geometry");
+  static_assert(S::X_DMA == 1 && S::W_DMA == 2 && S::T_DMA == 1, "DMA counts");
+  static_assert(S::XBUF == 8 * 1024 && S::WBUF == 16 * 1024, "partial tiles: 8 + 16 slots");
+  static constexpr int RUNM = S::LDS_BYTES;                  // u64[P / 64]: run starts
+  static constexpr int SEGM = RUNM + 8 * (kMoeMaxPairs / 64);  // u64[P / 64]: segment starts
+  static constexpr int XR = SEGM + 8 * (kMoeMaxPairs / 64);    // u16[P]: row, | 0x8000 invalid
+  static constexpr int SEGS = XR + 2 * kMoeMaxPairs;           // u16[P + 1]: segment starts
+  static constexpr int SEGE = SEGS + 2 * (kMoeMaxPairs + 2);   // u16[P]: segment expert
+  static constexpr int NSEG = SEGE + 2 * kMoeMaxPairs;
+  static constexpr int FLAG = NSEG + 4;  // int: this workgroup's piece completed its unit
+  static constexpr int BYTES = FLAG + 4;
+  static_assert(BYTES <= 80 * 1024, "two workgroups per CU");
+  static_assert(RUNM % 8 == 0 && NSEG % 4 == 0, "alignment");
+};
+
+template <typename Tag, int GS, bool GLU>
+__global__ __launch_bounds__(512) void moe_stream_kernel(GatherArgs a) {
+  using LY = MoeLayout<Tag, GS>;
+  using S = typename LY::S;
+  constexpr int OUTC = GLU ? 64 : 128;  // output columns per unit
+  constexpr int C_STEP_X = S::CK * 2;   // activation bytes per row and step
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kw = wave & 3, rg = wave >> 2;
+  uint64_t* t_run = reinterpret_cast<uint64_t*>(dfmi_smem + LY::RUNM);
+  uint64_t* t_segm = reinterpret_cast<uint64_t*>(dfmi_smem + LY::SEGM);
+  uint16_t* t_xr = reinterpret_cast<uint16_t*>(dfmi_smem + LY::XR);
+  uint16_t* t_seg = reinterpret_cast<uint16_t*>(dfmi_smem + LY::SEGS);
+  uint16_t* t_se = reinterpret_cast<uint16_t*>(dfmi_smem + LY::SEGE);
+  int* t_nseg = reinterpret_cast<int*>(dfmi_smem + LY::NSEG);
+  int* t_flag = reinterpret_cast<int*>(dfmi_smem + LY::FLAG);
+  const int P = a.P;
+  // the arguments as plain values (see gather_persist_kernel)
+  const uint16_t* const ax = a.x;
+  const int64_t x_rows = a.x_rows;
+  const uint32_t* const aw0 = a.w[0];
+  const uint32_t* const aw1 = a.w[1];
+  const uint32_t* const at = a.t;
+  const int32_t* const alhs = a.lhs;
+  const int32_t* const arhs = a.rhs;
+  uint16_t* const ay = a.y;
+  uint32_t* const wsc = a.ws_counters;
+  float* const wsp = a.ws_partials;
+  const int K = a.K, N = a.N, E = a.E;
+  const int NTC = GLU ? 2 * N : N;  // pair table columns per group
+
+  // --- segment table (P <= 256: pair p is thread p of wavefronts 0..3)
+  int e_p = 0;
+  bool st = false;  // pair tid starts a run
+  if (tid < P) {
+    const int l = alhs ? alhs[tid] : tid;
+    t_xr[tid] = (uint16_t)((l < 0 || l >= x_rows) ? 0x8000 : l);
+    e_p = arhs[tid];
+    st = tid == 0 || e_p != arhs[tid - 1];
+  }
+  if (wave < 4) {
+    const uint64_t m = __ballot(st);
+    if (lane == 0) t_run[wave] = m;
+  }
+  __syncthreads();
+  const int nw = (P + 63) / 64;
+  if (wave < nw) {  // segment starts: run starts and every 16th pair of a run
+    bool sg = false;
+    if (tid < P) {
+      int w = wave;
+      uint64_t m = t_run[w] & (lane == 63 ? ~0ull : ((2ull << lane) - 1ull));
+      while (m == 0) m = t_run[--w];  // ends: pair 0 starts a run
+      const int rs = 64 * w + 63 - __clzll((long long)m);
+      sg = ((tid - rs) & 15) == 0;
+    }
+    const uint64_t m2 = __ballot(sg);
+    if (lane == 0) t_segm[wave] = m2;
+  }
+  __syncthreads();
+  if (wave < nw) {  // compaction: each wavefront places its own segment starts
+    int base = 0;
+    for (int i = 0; i < wave; ++i) base += __popcll(t_segm[i]);
+    const uint64_t m = t_segm[wave];
+    if ((m >> lane) & 1ull) {
+      const int s = base + __popcll(m & ((1ull << lane) - 1ull));
+      t_seg[s] = (uint16_t)tid;
+      t_se[s] = (uint16_t)((e_p < 0 || e_p >= E) ? 0xFFFF : e_p);
+    }
+    if (wave == nw - 1 && lane == 0) {
+      const int total = base + __popcll(m);
+      t_seg[total] = (uint16_t)P;
+      *t_nseg = total;
+    }
+  }
+  __syncthreads();
+  const int nseg = __builtin_amdgcn_readfirstlane(*t_nseg);
+  const int ncb = N / OUTC;
+  const int units = nseg * ncb;
+  const int bid = blockIdx.x, G = gridDim.x;
+  const int H = G / 2, h = bid % H, sh = bid / H;  // CU h, slot sh
+  const int C = K / S::CK;  // steps per unit
+  // Tail split: with R whole rounds of H units, the r units of the last round
+  // are cut along K into SP pieces of PC = C / SP steps, one piece per CU, so
+  // every CU streams R units plus at most one piece; the pieces' partial
+  // tiles meet in the workspace and the last one to arrive finishes the unit.
+  // Only with a workspace and >= 4 steps per unit (a piece saves more than
+  // its exchange costs).
+  const int R = units / H, r = units - R * H;
+  int SP = 1;
+  if (wsc && r > 0 && C >= 4) {
+    SP = min(H / r, C / 2);
+    while (SP > 1 && C % SP) --SP;
+  }
+  SP = __builtin_amdgcn_readfirstlane(SP);
+  const int whole = SP > 1 ? R * H : units;
+  // whole units of this workgroup: h + H q with q = sh, sh + 2, ...
+  const int qmax = whole > h ? (whole - h + H - 1) / H : 0;
+  const int n_whole = qmax > sh ? (qmax - sh + 1) / 2 : 0;
+  // its piece (CU h < r SP): taken by the slot with fewer whole units
+  const bool has_piece = SP > 1 && h < r * SP && sh == (R & 1);
+  const int PC = C / SP;
+  const int nW = n_whole * C;                // steps of the whole units
+  const int V = nW + (has_piece ? PC : 0);  // this workgroup's steps
+  if (V == 0) return;                        // uniform
+  const int tu = h / SP, ppart = h - tu * SP;  // the piece: tail unit, part
+  auto unit_of = [&](int v) __attribute__((always_inline)) {  // unit of step v
+    return v < nW ? h + H * (2 * (v / C) + sh) : whole + tu;
+  };
+
+  const uint32_t wbytes = (uint32_t)N * (uint32_t)(K / 2);
+  const uint32_t wwords = wbytes / 4;
+  const uint32_t twords = (uint32_t)(K / GS) * (uint32_t)NTC;
+  // the unit being issued, as plain values carried across the loop
+  const uint32_t* iw0 = aw0;
+  const uint32_t* iw1 = aw1;
+  const uint32_t* it = at;
+  uint32_t lxg = kNoRow, lwg0 = 0, lwg1 = 0, ltg = kNoRow;
+  int ops = 0;  // loads (DMA instructions) this wavefront has issued
+  const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(ax, (uint32_t)x_rows * (uint32_t)K * 2u);
+  const __amdgpu_buffer_rsrc_t yr = buffer_rsrc(ay, (uint32_t)((int64_t)P * N * 2));
+  const DqConst dq = dq_const<Tag>();
+  const u32x4 ones = S::ones_operand();
+  // unit-independent fragment offsets
+  typename S::Lane L;
+  {
+    typename S::Ctx cx;
+    cx.x = xr;
+    cx.w = xr;
+    cx.t = xr;
+    cx.dense();
+    cx.K = K;
+    cx.M = 1;
+    cx.N = N;
+    cx.groups = K / GS;
+    cx.n0 = 0;
+    cx.lane = lane;
+    cx.wave = wave;
+    L = S::lane_setup(cx);
+  }
+  f32x4 acc[S::NT][1];
+
+  // Issue step vi: a unit's first step sets the unit's lane offsets.
+  auto issue = [&](int vi) __attribute__((always_inline)) {
+    const int c = __builtin_amdgcn_readfirstlane(vi < nW ? vi % C : ppart * PC + (vi - nW));
+    const int stage = __builtin_amdgcn_readfirstlane(vi % kPersistStages);
+    if (vi % C == 0) {  // a unit's (or the piece's) first step
+      const int u = __builtin_amdgcn_readfirstlane(unit_of(vi));
+      const int sidx = u / ncb;
+      const int cb = u - sidx * ncb;
+      const int p0 = __builtin_amdgcn_readfirstlane((int)t_seg[sidx]);
+      const int rows = __builtin_amdgcn_readfirstlane((int)t_seg[sidx + 1]) - p0;
+      const int e = __builtin_amdgcn_readfirstlane((int)t_se[sidx]);
+      const size_t ee = e == 0xFFFF ? 0 : (size_t)e;
+      iw0 = aw0 + ee * wwords;
+      iw1 = aw1 + ee * wwords;
+      it = at + ee * twords;
+      const int n0 = cb * OUTC;
+      {  // activation rows 2 wave, 2 wave + 1; lane piece (lane % 32) ^ (row & 15)
+        const int r = 2 * wave + (lane >> 5);
+        const int piece = (lane & 31) ^ (r & 15);
+        const int xrow = t_xr[p0 + min(r, rows - 1)] & 0x7fff;
+        lxg = r < rows ? (uint32_t)xrow * (uint32_t)K * 2u + (uint32_t)piece * 16u : kNoRow;
+      }
+      {  // weight rows (2 wave + i) * 8 + lane / 8; piece (lane % 8) ^ (row % 8)
+        uint32_t wg[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int R = (2 * wave + i) * 8 + (lane >> 3);
+          const int piece = (lane & 7) ^ (R & 7);
+          const int n = GLU ? n0 + 32 * (R >> 6) + (R & 31) : n0 + R;
+          wg[i] = (uint32_t)n * (uint32_t)(K / 2) + (uint32_t)piece * 16u;
+        }
+        lwg0 = wg[0];
+        lwg1 = wg[1];
+      }
+      {  // pairs: stage bytes wave TPB + 16 lane = group o / 512, rows (o % 512) / 4 ..
+        const int o = wave * S::TPB + 16 * lane;
+        const int col = (GLU ? 2 * n0 : n0) + (o % (4 * S::NB)) / 4;
+        ltg = lane < S::TLANES
+                  ? ((uint32_t)(o / (4 * S::NB)) * (uint32_t)NTC + (uint32_t)col) * 4u
+                  : kNoRow;
+      }
+    }
+    dma16(xr, lxg, (uint32_t)c * (uint32_t)C_STEP_X,
+          dfmi_smem + S::X_OFF + stage * S::XBUF + wave * 1024);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int r0 = (2 * wave + i) * 8;  // wave-uniform
+      const uint32_t* base = (GLU && (r0 & 63) >= 32) ? iw1 : iw0;
+      dma16(buffer_rsrc(base, wbytes), i ? lwg1 : lwg0, (uint32_t)c * (uint32_t)S::WROW,
+            dfmi_smem + S::W_OFF + stage * S::WBUF + r0 * S::WROW);
+    }
+    if (lane < S::TLANES)
+      dma16(buffer_rsrc(it, twords * 4u), ltg, (uint32_t)c * (uint32_t)(S::GPC * 4 * NTC),
+            dfmi_smem + S::T_OFF + stage * S::SBS + wave * S::TPB);
+    ops += S::CHUNK_DMA;
+  };
+  // Wait until step v has landed: the loads issued after it are its
+  // successors' (uncounted output stores only lengthen a wait).
+  auto wait_chunk = [&](int v) __attribute__((always_inline)) {
+    stage_barrier_n(ops - (v + 1) * S::CHUNK_DMA);
+  };
+  auto read = [&](int v, typename S::Frag& f) __attribute__((always_inline)) {
+    typename S::Ctx cr;
+    cr.wave = wave;
+    cr.sb_base = 0;
+    S::read_frag(cr, L, 0, __builtin_amdgcn_readfirstlane(v % kPersistStages), 0, f);
+  };
+  // Partial tile slot k (0 .. 23) of the free stage: 8 in its activation
+  // part, 16 in its weight part.
+  auto slot_ptr = [&](int slot, int k) __attribute__((always_inline)) {
+    return reinterpret_cast<float*>(
+        dfmi_smem + (k < 8 ? S::X_OFF + slot * S::XBUF + k * 1024
+                           : S::W_OFF + slot * S::WBUF + (k - 8) * 1024));
+  };
+  // Outputs of the unit that ends at step v (the stage of the step after it
+  // is free: its fragments are in registers and its next DMA follows the
+  // next barrier).  A piece instead publishes its partial tiles; the last
+  // piece of a unit to arrive sums all of them in part order and finishes.
+  auto epilogue = [&](int v, int slot) __attribute__((always_inline)) {
+    const bool piece = v >= nW;  // uniform: the workgroup's last work item
+    const int u = __builtin_amdgcn_readfirstlane(unit_of(v));
+    const int sidx = u / ncb;
+    const int cb = u - sidx * ncb;
+    const int p0 = __builtin_amdgcn_readfirstlane((int)t_seg[sidx]);
+    const int rows = __builtin_amdgcn_readfirstlane((int)t_seg[sidx + 1]) - p0;
+    const bool bad_e = __builtin_amdgcn_readfirstlane((int)t_se[sidx]) == 0xFFFF;
+    const int n0 = cb * OUTC;
+    stage_barrier<15>();  // every wavefront's fragment reads of that stage have returned
+#pragma unroll
+    for (int T = 0; T < 4; ++T) {
+      const int fin = GLU ? (T & 1) : T;  // the finishing wavefront of tile T
+      if (fin != kw) {
+        const int k = rg * 12 + T * 3 + (kw < fin ? kw : kw - 1);
+        float* dst = slot_ptr(slot, k);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) dst[q * 64 + lane] = acc[T][0][q];
+      }
+    }
+    stage_barrier<15>();
+    const bool finisher = GLU ? kw < 2 : true;
+    // the finished tiles (tile kw, and kw + 2 for the SwiGLU): this
+    // wavefront's own partials, selected without indexing registers, plus
+    // the other three wavefronts'
+    float g[4], up[4];
+    if (finisher) {
+      f32x4 own0, own1;
+      if constexpr (GLU) {
+        own0 = kw == 0 ? acc[0][0] : acc[1][0];
+        own1 = kw == 0 ? acc[2][0] : acc[3][0];
+      } else {
+        own0 = kw == 0 ? acc[0][0] : (kw == 1 ? acc[1][0] : (kw == 2 ? acc[2][0] : acc[3][0]));
+        own1 = own0;
+      }
+      const int k0 = rg * 12 + kw * 3, k1 = rg * 12 + (kw + 2) * 3;  // their slots
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        g[q] = own0[q];
+        up[q] = own1[q];
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+          g[q] += slot_ptr(slot, k0 + i)[q * 64 + lane];
+          if (GLU) up[q] += slot_ptr(slot, k1 + i)[q * 64 + lane];
+        }
+      }
+    }
+    if (piece) {
+      // partial tiles of part ppart: [tail unit][part][row group][tile][reg][lane]
+      float* mine = wsp + ((size_t)(tu * SP + ppart) * 2 + rg) * 1024;
+      if (finisher) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          __hip_atomic_store(mine + (kw * 4 + q) * 64 + lane, g[q], __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+          if (GLU)
+            __hip_atomic_store(mine + ((kw + 2) * 4 + q) * 64 + lane, up[q], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+      stage_barrier<0>();  // every partial store of the workgroup has completed
+      if (tid == 0) {
+        const unsigned prev =
+            __hip_atomic_fetch_add(&wsc[tu], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *t_flag = prev == (unsigned)(SP - 1) ? 1 : 0;
+      }
+      stage_barrier<0>();
+      if (!__builtin_amdgcn_readfirstlane(*t_flag)) return;
+      if (finisher) {
+        const float* first = wsp + ((size_t)tu * SP * 2 + rg) * 1024;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) g[q] = up[q] = 0.f;
+        for (int p = 0; p < SP; ++p) {  // part order: independent of arrival order
+          const float* pp = first + (size_t)p * 2 * 1024;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            g[q] += __hip_atomic_load(pp + (kw * 4 + q) * 64 + lane, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
+            if (GLU)
+              up[q] += __hip_atomic_load(pp + ((kw + 2) * 4 + q) * 64 + lane, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+          }
+        }
+      }
+      if (tid == 0) __hip_atomic_exchange(&wsc[tu], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (finisher) {
+      const int col = lane & 15, kg = lane >> 4;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int m = 4 * kg + q;
+        const int n = GLU ? n0 + 32 * rg + 16 * kw + col : n0 + 64 * rg + 16 * kw + col;
+        const int xrow = t_xr[p0 + min(m, rows - 1)];
+        float out;
+        if (bad_e || (xrow & 0x8000)) {
+          out = __builtin_nanf("");
+        } else if (GLU) {
+          out = silu_mul<Tag>(rnd<Tag>(g[q]), rnd<Tag>(up[q]));
+        } else {
+          out = g[q];
+        }
+        const uint32_t off =
+            m < rows ? (uint32_t)(((int64_t)(p0 + m) * N + n) * 2) : kNoRow;
+        __builtin_amdgcn_raw_buffer_store_b16(Num<Tag>::f2h(out), yr, off, 0, 0);
+      }
+    }
+  };
+
+  for (int k = 0; k < kPersistStages && k < V; ++k) issue(k);
+  wait_chunk(0);
+  typename S::Frag fa, fb;
+  read(0, fa);
+#define DFMI_MOE_STEP(v, CUR, NXT)                                            \
+  do {                                                                        \
+    if ((v) + 1 < V) {                                                        \
+      wait_chunk((v) + 1);                                                    \
+      if ((v) + kPersistStages < V) issue((v) + kPersistStages);              \
+      read((v) + 1, NXT);                                                     \
+    }                                                                         \
+    if ((v) % C == 0) {                                                       \
+      _Pragma("unroll") for (int t = 0; t < S::NT; ++t) acc[t][0] = zero4(); \
+    }                                                                         \
+    S::compute(L, CUR, acc, dq, ones);                                        \
+    if ((v) % C == C - 1 || (v) == V - 1)                                      \
+      epilogue((v), ((v) + 1) % kPersistStages);                              \
+  } while (0)
+  int v = 0;
+  for (; v + 1 < V; v += 2) {
+    DFMI_MOE_STEP(v, fa, fb);
+    DFMI_MOE_STEP(v + 1, fb, fa);
+  }
+  if (v < V) DFMI_MOE_STEP(v, fa, fb);
+#undef DFMI_MOE_STEP
+}
+
+template <typename Tag, int GS, bool GLU>
+static void launch_moe_stream_t(const GatherArgs& a, int grid, hipStream_t st) {
+  using LY = MoeLayout<Tag, GS>;
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(&moe_stream_kernel<Tag, GS, GLU>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, LY::BYTES);
+  (void)attr;
+  hipLaunchKernelGGL((moe_stream_kernel<Tag, GS, GLU>), dim3(grid), dim3(512), LY::BYTES, st, a);
+}
+
+template <typename Tag, bool GLU>
+static void launch_moe_stream(const GatherArgs& a, int gs, int grid, hipStream_t st) {
+  if (gs == 64) launch_moe_stream_t<Tag, 64, GLU>(a, grid, st);
+  else launch_moe_stream_t<Tag, 128, GLU>(a, grid, st);
+}
+
 template <typename Tag, int GS, bool GLU>
 static void launch_gather_persist_t(const GatherArgs& a, hipStream_t st) {
   using LY = PersistLayout<Tag, GS>;
@@ -638,6 +1064,19 @@ static void launch_gather(const GatherArgs& a, int gs, bool kfull, int nt, int n
   else launch_gather_gs<Tag, 128, GLU>(a, kfull, nt, n_blocks, waves, st);
 }
 
+// Shapes moe_stream_kernel takes (with a pair table): 4-bit weights (checked
+// by the caller), gs 64 / 128, whole 256-k steps, whole units of 64 (SwiGLU)
+// or 128 output columns, at most kMoeMaxPairs pairs, 16-bit row and expert
+// ids, 32-bit buffer offsets.
+static bool moe_stream_eligible(int64_t x_rows, int64_t P, int64_t K, int64_t N, int64_t E,
+                                int gs, bool glu) {
+  const int64_t ntc = glu ? 2 * N : N;
+  return (gs == 64 || gs == 128) && K >= 256 && K % 256 == 0 && N > 0 &&
+         N % (glu ? 64 : 128) == 0 && P >= 1 && P <= kMoeMaxPairs && x_rows <= 32767 &&
+         E < 65535 && x_rows * K * 2 < (1ll << 31) && N * (K / 2) < (1ll << 31) &&
+         (K / gs) * ntc * 4 < (1ll << 31) && P * N * 2 < (1ll << 31);
+}
+
 static int validate_gather(int x_dtype, int64_t x_rows, int64_t P, int64_t K, int64_t N,
                            int64_t E, int gs, int bits) {
   if (x_dtype != DFMI_BF16 && x_dtype != DFMI_F16) {
@@ -671,7 +1110,8 @@ static int gather_common(const void* x, int x_dtype, int64_t x_rows, const uint3
                          const void* s0, const void* b0, const uint32_t* w1, const void* s1,
                          const void* b1, const int32_t* lhs_rows, const int32_t* rhs_experts,
                          void* y, int64_t P, int64_t K, int64_t N, int64_t E, int group_size,
-                         int bits, bool glu, void* stream) {
+                         int bits, bool glu, const uint32_t* pairs, void* workspace,
+                         size_t workspace_bytes, void* stream) {
   int rc = validate_gather(x_dtype, x_rows, P, K, N, E, group_size, bits);
   if (rc != DFMI_OK) return rc;
   if (P == 0 || N == 0) return DFMI_OK;
@@ -701,7 +1141,27 @@ static int gather_common(const void* x, int x_dtype, int64_t x_rows, const uint3
   a.N = (int)N;
   a.E = (int)E;
   a.chunks = (int)((K + kChunkK - 1) / kChunkK);
+  a.t = pairs;
+  const bool ws_ok = workspace && workspace_bytes >= kMoeWsBytes && aligned16(workspace);
+  a.ws_counters = ws_ok ? static_cast<uint32_t*>(workspace) : nullptr;
+  a.ws_partials =
+      ws_ok ? reinterpret_cast<float*>(static_cast<char*>(workspace) + kMoeWsCounterBytes) : nullptr;
   hipStream_t st = static_cast<hipStream_t>(stream);
+  // pair-streaming persistent loop (a pair table given): whole 256-k steps,
+  // 128-row units, two workgroups per CU, the pair ids in 16-bit LDS tables.
+  if (pairs && aligned16(pairs) && moe_stream_eligible(x_rows, P, K, N, E, group_size, glu)) {
+    const int64_t units_max = P * (N / (glu ? 64 : 128));  // segments <= pairs
+    const int grid =
+        (int)std::min<int64_t>(kMoeGroups, std::max<int64_t>(2, (units_max + 1) & ~1ll));
+    if (glu) {
+      if (x_dtype == DFMI_BF16) launch_moe_stream<BF16, true>(a, group_size, grid, st);
+      else launch_moe_stream<F16, true>(a, group_size, grid, st);
+    } else {
+      if (x_dtype == DFMI_BF16) launch_moe_stream<BF16, false>(a, group_size, grid, st);
+      else launch_moe_stream<F16, false>(a, group_size, grid, st);
+    }
+    return check_launch(glu ? "dfmi_gather_qmm_swiglu" : "dfmi_gather_qmm_affine");
+  }
   // persistent pipelined loop: whole 512-k steps, a full-K scale window of
   // at most 4 pieces, the pair tables in LDS, 32-bit buffer offsets.
   // Measured on MI355X (16 tokens, top-8 of 256 experts, 40 layers): the
@@ -782,8 +1242,23 @@ extern "C" int dfmi_gather_qmm_affine(const void* x, int x_dtype, int64_t x_rows
                                       void* y, int64_t P, int64_t K, int64_t N, int64_t E,
                                       int group_size, int bits, void* stream) {
   return gather_common(x, x_dtype, x_rows, w_q, scales, biases, nullptr, nullptr, nullptr,
-                       lhs_rows, rhs_experts, y, P, K, N, E, group_size, bits, false, stream);
+                       lhs_rows, rhs_experts, y, P, K, N, E, group_size, bits, false, nullptr,
+                       nullptr, 0, stream);
 }
+
+extern "C" int dfmi_gather_qmm_affine_pairs(const void* x, int x_dtype, int64_t x_rows,
+                                            const uint32_t* w_q, const void* scales,
+                                            const void* biases, const uint32_t* sb_pairs,
+                                            const int32_t* lhs_rows, const int32_t* rhs_experts,
+                                            void* y, int64_t P, int64_t K, int64_t N, int64_t E,
+                                            int group_size, int bits, void* workspace,
+                                            size_t workspace_bytes, void* stream) {
+  return gather_common(x, x_dtype, x_rows, w_q, scales, biases, nullptr, nullptr, nullptr,
+                       lhs_rows, rhs_experts, y, P, K, N, E, group_size, bits, false, sb_pairs,
+                       workspace, workspace_bytes, stream);
+}
+
+extern "C" size_t dfmi_gather_workspace_bytes(void) { return kMoeWsBytes; }
 
 extern "C" int dfmi_gather_qmm_swiglu(const void* x, int x_dtype, int64_t x_rows,
                                       const uint32_t* wg_q, const void* g_scales,
@@ -793,7 +1268,84 @@ extern "C" int dfmi_gather_qmm_swiglu(const void* x, int x_dtype, int64_t x_rows
                                       void* h, int64_t P, int64_t K, int64_t N, int64_t E,
                                       int group_size, int bits, void* stream) {
   return gather_common(x, x_dtype, x_rows, wg_q, g_scales, g_biases, wu_q, u_scales, u_biases,
-                       lhs_rows, rhs_experts, h, P, K, N, E, group_size, bits, true, stream);
+                       lhs_rows, rhs_experts, h, P, K, N, E, group_size, bits, true, nullptr,
+                       nullptr, 0, stream);
+}
+
+extern "C" int dfmi_gather_qmm_swiglu_pairs(const void* x, int x_dtype, int64_t x_rows,
+                                            const uint32_t* wg_q, const void* g_scales,
+                                            const void* g_biases, const uint32_t* wu_q,
+                                            const void* u_scales, const void* u_biases,
+                                            const uint32_t* sb_pairs, const int32_t* lhs_rows,
+                                            const int32_t* rhs_experts, void* h, int64_t P,
+                                            int64_t K, int64_t N, int64_t E, int group_size,
+                                            int bits, void* workspace, size_t workspace_bytes,
+                                            void* stream) {
+  return gather_common(x, x_dtype, x_rows, wg_q, g_scales, g_biases, wu_q, u_scales, u_biases,
+                       lhs_rows, rhs_experts, h, P, K, N, E, group_size, bits, true, sb_pairs,
+                       workspace, workspace_bytes, stream);
+}
+
+// Pair tables of expert weights: [E][G][N] from one (scales, biases) set, or
+// for the SwiGLU [E][G][2N] interleaving the gate and up sets 32 columns at a
+// time (table column 64 (n / 32) + 32 up + n % 32).  Each workgroup
+// transposes 64 table columns x 64 groups of one expert through LDS.
+__global__ __launch_bounds__(256) void moe_pairs_kernel(const uint16_t* s0, const uint16_t* b0,
+                                                        const uint16_t* s1, const uint16_t* b1,
+                                                        uint32_t* t, int N, int G) {
+  __shared__ uint32_t tile[64][65];
+  const bool glu = s1 != nullptr;
+  const int ntc = glu ? 2 * N : N;
+  const int c0 = blockIdx.x * 64, g0 = blockIdx.y * 64;
+  const int64_t e = blockIdx.z;
+  for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+    const int r = i / 64, gi = i % 64;  // table column c0 + r, group g0 + gi
+    const int c = c0 + r, g = g0 + gi;
+    uint32_t v = 0;
+    if (c < ntc && g < G) {
+      const bool up = glu && (c & 32);
+      const int n = glu ? 32 * (c >> 6) + (c & 31) : c;
+      const int64_t o = (e * N + n) * G + g;
+      const uint16_t sv = up ? s1[o] : s0[o];
+      const uint16_t bv = up ? b1[o] : b0[o];
+      v = (uint32_t)sv | ((uint32_t)bv << 16);
+    }
+    tile[r][gi] = v;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+    const int gi = i / 64, r = i % 64;
+    const int c = c0 + r, g = g0 + gi;
+    if (c < ntc && g < G) t[(e * G + g) * ntc + c] = tile[r][gi];
+  }
+}
+
+extern "C" int dfmi_moe_pairs(const void* scales, const void* biases, const void* up_scales,
+                              const void* up_biases, int dtype, int64_t E, int64_t N,
+                              int64_t groups, uint32_t* sb_pairs, void* stream) {
+  if (dtype != DFMI_BF16 && dtype != DFMI_F16) {
+    set_error("dfmi_moe_pairs: dtype %d unsupported (bf16 or f16)", dtype);
+    return DFMI_EINVAL;
+  }
+  const bool glu = up_scales != nullptr || up_biases != nullptr;
+  if (E < 0 || N < 0 || groups < 0 || E > 65535 || N >= (1ll << 30) || groups >= (1ll << 30) ||
+      (glu && N % 32 != 0) || E * N * groups * (glu ? 2 : 1) >= (1ll << 40)) {
+    set_error("dfmi_moe_pairs: bad shape E=%lld N=%lld groups=%lld%s", (long long)E,
+              (long long)N, (long long)groups, glu ? " (SwiGLU: N a multiple of 32)" : "");
+    return DFMI_EINVAL;
+  }
+  if (E == 0 || N == 0 || groups == 0) return DFMI_OK;
+  if (!scales || !biases || !sb_pairs || (glu && (!up_scales || !up_biases))) {
+    set_error("dfmi_moe_pairs: null pointer");
+    return DFMI_EINVAL;
+  }
+  const int64_t ntc = glu ? 2 * N : N;
+  const dim3 grid((unsigned)((ntc + 63) / 64), (unsigned)((groups + 63) / 64), (unsigned)E);
+  hipLaunchKernelGGL(moe_pairs_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const uint16_t*>(scales), static_cast<const uint16_t*>(biases),
+                     static_cast<const uint16_t*>(up_scales),
+                     static_cast<const uint16_t*>(up_biases), sb_pairs, (int)N, (int)groups);
+  return check_launch("dfmi_moe_pairs");
 }
 
 extern "C" int dfmi_moe_combine(const void* y, int y_dtype, const int32_t* y_rows,

@@ -16,6 +16,13 @@ pair ``p = t*k + j`` reads activation row ``t`` (or ``lhs_indices[p]``) and
 expert ``rhs_indices[p]``.  ``gather_qmm`` is ``dfmi_gather_qmm_affine``,
 the gate/up pair plus SwiGLU is one ``dfmi_gather_qmm_swiglu`` launch (one
 pass over both weight sets), and the weighted sum is ``dfmi_moe_combine``.
+
+Where the expert shapes allow (4-bit, gs 64 / 128, K a multiple of 256,
+N a multiple of 128, or 64 for the SwiGLU pair, at most 256 pairs) the
+gathers take the experts' (scale, bias) pair table (``dfmi_moe_pairs``,
+built once per weight set and cached) and the stream's gather workspace, and
+run the pair-streaming main loop (``dfmi_gather_qmm_*_pairs``); otherwise,
+and during graph capture before a table exists, the plain entry points.
 """
 
 from __future__ import annotations
@@ -49,17 +56,49 @@ def _expert_weights(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
             _runtime.aligned_contiguous(biases))
 
 
+def _pairs_ptr(pairs: Optional[torch.Tensor], scales: torch.Tensor, biases: torch.Tensor,
+               up: Optional[Tuple[torch.Tensor, torch.Tensor]], K: int, N: int,
+               group_size: int, bits: int, use_pairs: bool):
+    """Address of the experts' pair table (``dfmi_moe_pairs`` layout), or None.
+
+    An explicit table is checked for shape and device; otherwise the cached
+    table of these scales / biases is used when the shape takes one (built on
+    first use, never during graph capture)."""
+    E, _, G = (int(d) for d in scales.shape)
+    cols = 2 * N if up is not None else N
+    if pairs is not None:
+        _runtime.require_device(pairs, "pairs")
+        if (pairs.dtype != torch.int32 or tuple(pairs.shape) != (E, G, cols)
+                or not pairs.is_contiguous()):
+            raise ValueError(f"pairs must be a contiguous int32 [{E}, {G}, {cols}] table")
+        return pairs.data_ptr()
+    if not use_pairs or not _runtime.moe_pair_shape(K, N, group_size, bits, up is not None):
+        return None
+    table = _runtime.PAIRS.get(scales, biases, up, experts=True)
+    return table.data_ptr() if table is not None else None
+
+
+def _workspace(lib, device: torch.device, table_ptr):
+    """The stream's gather workspace (tail-split counters and partials), only
+    with a pair table (the plain main loops take none)."""
+    if table_ptr is None:
+        return None, 0
+    return _runtime.workspace(device, int(lib.dfmi_gather_workspace_bytes()), kind="gather")
+
+
 def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
                rhs_indices: torch.Tensor, *, lhs_indices: Optional[torch.Tensor] = None,
                transpose: bool = True, group_size: int = 64, bits: int = 4,
-               sorted_indices: bool = False) -> torch.Tensor:
+               sorted_indices: bool = False, pairs: Optional[torch.Tensor] = None,
+               use_pairs: bool = True) -> torch.Tensor:
     """``y[p] = x[lhs[p]] . dequant(W[rhs[p]])^T`` for every pair p.
 
     ``x`` ``[R, K]`` (bf16/f16), ``w`` ``[E, N, K*bits/32]`` uint32,
     ``rhs_indices`` ``[P]`` expert ids, ``lhs_indices`` ``[P]`` row ids or
     None (row p).  Returns ``[P, N]`` in x's dtype.  ``sorted_indices`` is
     accepted for signature parity: runs of equal experts are found on the
-    device either way.
+    device either way.  ``pairs`` / ``use_pairs``: the experts' pair table
+    (``dfmi_gather_qmm_affine_pairs``), by default the cached one.
     """
     del sorted_indices
     if not transpose:
@@ -75,21 +114,26 @@ def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: t
     if lhs is not None and int(lhs.shape[0]) != P:
         raise ValueError("lhs_indices and rhs_indices must have the same length")
     y = torch.empty((P, N), dtype=x.dtype, device=x.device)
+    tp = _pairs_ptr(pairs, scales, biases, None, K, N, group_size, bits, use_pairs)
     lib = _lib.load()
-    _lib.check(lib.dfmi_gather_qmm_affine(
+    ws, ws_bytes = _workspace(lib, x.device, tp)
+    _lib.check(lib.dfmi_gather_qmm_affine_pairs(
         x2.data_ptr(), _runtime.dtype_code(x.dtype), int(x2.shape[0]), w.data_ptr(),
-        scales.data_ptr(), biases.data_ptr(), lhs.data_ptr() if lhs is not None else None,
-        rhs.data_ptr(), y.data_ptr(), P, K, N, E, int(group_size), int(bits),
-        _runtime.stream_ptr(x.device)), "dfmi_gather_qmm_affine")
+        scales.data_ptr(), biases.data_ptr(), tp, lhs.data_ptr() if lhs is not None else None,
+        rhs.data_ptr(), y.data_ptr(), P, K, N, E, int(group_size), int(bits), ws, ws_bytes,
+        _runtime.stream_ptr(x.device)), "dfmi_gather_qmm_affine_pairs")
     return y
 
 
 def gather_swiglu(x: torch.Tensor, gate: Triple, up: Triple, rhs_indices: torch.Tensor, *,
                   lhs_indices: Optional[torch.Tensor] = None, group_size: int = 64,
-                  bits: int = 4) -> torch.Tensor:
+                  bits: int = 4, pairs: Optional[torch.Tensor] = None,
+                  use_pairs: bool = True) -> torch.Tensor:
     """``silu(gather_qmm(x, gate)) * gather_qmm(x, up)`` per pair in one
     weight pass (each product rounded to x's dtype first, then the MLX
-    op-by-op SwiGLU rounding).  Returns ``[P, N]``."""
+    op-by-op SwiGLU rounding).  Returns ``[P, N]``.  ``pairs`` /
+    ``use_pairs``: the interleaved gate/up pair table
+    (``dfmi_gather_qmm_swiglu_pairs``), by default the cached one."""
     _runtime.require_device(x, "x")
     K = int(x.shape[-1])
     x2 = _runtime.aligned_contiguous(x.reshape(-1, K))
@@ -101,12 +145,15 @@ def gather_swiglu(x: torch.Tensor, gate: Triple, up: Triple, rhs_indices: torch.
     lhs = _indices(lhs_indices, "lhs_indices")
     P = int(rhs.shape[0])
     h = torch.empty((P, N), dtype=x.dtype, device=x.device)
+    tp = _pairs_ptr(pairs, sg, bg, (su, bu), K, N, group_size, bits, use_pairs)
     lib = _lib.load()
-    _lib.check(lib.dfmi_gather_qmm_swiglu(
+    ws, ws_bytes = _workspace(lib, x.device, tp)
+    _lib.check(lib.dfmi_gather_qmm_swiglu_pairs(
         x2.data_ptr(), _runtime.dtype_code(x.dtype), int(x2.shape[0]), wg.data_ptr(),
-        sg.data_ptr(), bg.data_ptr(), wu.data_ptr(), su.data_ptr(), bu.data_ptr(),
+        sg.data_ptr(), bg.data_ptr(), wu.data_ptr(), su.data_ptr(), bu.data_ptr(), tp,
         lhs.data_ptr() if lhs is not None else None, rhs.data_ptr(), h.data_ptr(), P, K, N,
-        Eg, int(group_size), int(bits), _runtime.stream_ptr(x.device)), "dfmi_gather_qmm_swiglu")
+        Eg, int(group_size), int(bits), ws, ws_bytes, _runtime.stream_ptr(x.device)),
+        "dfmi_gather_qmm_swiglu_pairs")
     return h
 
 

@@ -259,6 +259,52 @@ int dfmi_gather_qmm_swiglu(const void *x, int x_dtype, int64_t x_rows,
                            void *stream);
 
 /*
+ * The two gathers above with the experts' (scale, bias) pair table
+ * (dfmi_moe_pairs): the same results within the gathers' tolerance, from a
+ * main loop that streams the pairs per 256-k step (128-row work units, two
+ * workgroups per CU).  Taken when sb_pairs != NULL (16-byte aligned), gs is
+ * 64 or 128, K % 256 == 0, N % 128 == 0 (affine) or N % 64 == 0 (SwiGLU),
+ * P <= 256, x_rows <= 32767 and E < 65535; otherwise the call is exactly the
+ * plain entry point's.  Same call sites as dfmi_gather_qmm_affine /
+ * dfmi_gather_qmm_swiglu (mlx-lm QuantizedSwitchLinear / SwitchGLU, reached
+ * from dflash_mlx/engine/target_qwen_gdn.py:865,874), with the per-layer
+ * table built once, as the reference's VerifyQuantizedLinear precomputes
+ * per-module state (dflash_mlx/verify_linear.py:118-223).
+ * workspace (16-byte aligned, dfmi_gather_workspace_bytes() bytes, zero
+ * when first used; the call leaves it zero) lets the units of the last
+ * partial round split along K; NULL runs them whole.  Calls that overlap
+ * on one workspace race.
+ */
+int dfmi_gather_qmm_affine_pairs(const void *x, int x_dtype, int64_t x_rows,
+                                 const uint32_t *w_q, const void *scales, const void *biases,
+                                 const uint32_t *sb_pairs, const int32_t *lhs_rows,
+                                 const int32_t *rhs_experts, void *y, int64_t P, int64_t K,
+                                 int64_t N, int64_t E, int group_size, int bits,
+                                 void *workspace, size_t workspace_bytes, void *stream);
+int dfmi_gather_qmm_swiglu_pairs(const void *x, int x_dtype, int64_t x_rows,
+                                 const uint32_t *wg_q, const void *g_scales,
+                                 const void *g_biases, const uint32_t *wu_q,
+                                 const void *u_scales, const void *u_biases,
+                                 const uint32_t *sb_pairs, const int32_t *lhs_rows,
+                                 const int32_t *rhs_experts, void *h, int64_t P, int64_t K,
+                                 int64_t N, int64_t E, int group_size, int bits,
+                                 void *workspace, size_t workspace_bytes, void *stream);
+size_t dfmi_gather_workspace_bytes(void);
+
+/*
+ * Pair table of routed experts for the *_pairs gathers: from scales / biases
+ * [E, N, groups] (16-bit, dtype DFMI_BF16 or DFMI_F16), sb_pairs
+ * [E][groups][N] uint32 = scale | bias << 16.  With up_scales / up_biases
+ * (the SwiGLU's up projection; N a multiple of 32) the table is
+ * [E][groups][2N], gate and up interleaved 32 columns at a time: column
+ * 64 (n / 32) + 32 u + n % 32 holds row n of the gate (u = 0) or up (u = 1)
+ * set.  Asynchronous on `stream`.
+ */
+int dfmi_moe_pairs(const void *scales, const void *biases, const void *up_scales,
+                   const void *up_biases, int dtype, int64_t E, int64_t N, int64_t groups,
+                   uint32_t *sb_pairs, void *stream);
+
+/*
  * Weighted sum over each token's top-k expert outputs (the Qwen MoE block's
  * `(y * scores[..., None]).sum(axis=-2)`, reached from
  * dflash_mlx/engine/target_qwen_gdn.py:865,874), with the unsort mlx-lm's
