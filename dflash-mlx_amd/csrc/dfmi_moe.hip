@@ -855,9 +855,7 @@ __global__ __launch_bounds__(512) void moe_stream_kernel(GatherArgs a) {
       const int fin = GLU ? (T & 1) : T;  // the finishing wavefront of tile T
       if (fin != kw) {
         const int k = rg * 12 + T * 3 + (kw < fin ? kw : kw - 1);
-        float* dst = slot_ptr(slot, k);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) dst[q * 64 + lane] = acc[T][0][q];
+        reinterpret_cast<f32x4*>(slot_ptr(slot, k))[lane] = acc[T][0];  // one 16-byte write
       }
     }
     stage_barrier<15>();
@@ -880,10 +878,16 @@ __global__ __launch_bounds__(512) void moe_stream_kernel(GatherArgs a) {
       for (int q = 0; q < 4; ++q) {
         g[q] = own0[q];
         up[q] = own1[q];
+      }
 #pragma unroll
-        for (int i = 0; i < 3; ++i) {
-          g[q] += slot_ptr(slot, k0 + i)[q * 64 + lane];
-          if (GLU) up[q] += slot_ptr(slot, k1 + i)[q * 64 + lane];
+      for (int i = 0; i < 3; ++i) {  // one 16-byte read per partial tile
+        const f32x4 a = reinterpret_cast<const f32x4*>(slot_ptr(slot, k0 + i))[lane];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) g[q] += a[q];
+        if (GLU) {
+          const f32x4 b = reinterpret_cast<const f32x4*>(slot_ptr(slot, k1 + i))[lane];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) up[q] += b[q];
         }
       }
     }
@@ -930,6 +934,7 @@ __global__ __launch_bounds__(512) void moe_stream_kernel(GatherArgs a) {
       const int col = lane & 15, kg = lane >> 4;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
+        if (q >= rows) break;  // uniform: no lane of the wavefront holds an output row
         const int m = 4 * kg + q;
         const int n = GLU ? n0 + 32 * rg + 16 * kw + col : n0 + 64 * rg + 16 * kw + col;
         const int xrow = t_xr[p0 + min(m, rows - 1)];
