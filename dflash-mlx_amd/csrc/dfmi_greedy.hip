@@ -218,7 +218,7 @@ __global__ __launch_bounds__(64 * WV) void lmhead_stream_kernel(LmArgs a) {
   for (int t = 0; t < S::NT; ++t)
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[t][mt] = zero4();
-  S::run(cx, 0, a.K / S::CK, acc);
+  S::template run<true>(cx, 0, a.K / S::CK, acc);  // bias terms batched into MFMAs
 
   // sum the partial tiles of each row group's KW wavefronts through LDS (the
   // stages are free: every DMA has landed and every wavefront is past its

@@ -523,6 +523,77 @@ struct Stream {
     }
   }
 
+  // Bias terms (b - OFF s) X of up to four steps, applied by one fp32 MFMA
+  // (16x16x4: D[m][n] += sum over the batch of A[m][slot] B[slot][n])
+  // instead of four FMAs per accumulator and step: lane (col, kg) records,
+  // for the step in batch slot kg, X of activation row col (A operand) and
+  // b - OFF s of weight row col (B operand).  Slots not yet written hold 0.
+  // Two k-blocks per group (gs >= 64) only; gs = 32 keeps the FMAs.
+  struct Bias {
+    float ax[MT];
+    float bb[NT];
+  };
+  __device__ static inline void bias_zero(Bias& z) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) z.ax[mt] = 0.f;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) z.bb[t] = 0.f;
+  }
+  __device__ static inline void bias_flush(Bias& z, f32x4 (&acc)[NT][MT]) {
+    if constexpr (PAIR) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          acc[t][mt] = __builtin_amdgcn_mfma_f32_16x16x4f32(z.ax[mt], z.bb[t], acc[t][mt], 0, 0, 0);
+      bias_zero(z);
+    }
+  }
+
+  // compute() with the step's bias terms recorded in z (mine: this lane's kg
+  // is the step's batch slot); the caller flushes z after the fourth step of
+  // a batch and after the last step of a range.
+  __device__ static inline void compute_b(const Lane& L, const Frag& f, f32x4 (&acc)[NT][MT],
+                                          const DqConst& dq, const u32x4 ones, Bias& z,
+                                          const bool mine) {
+    if constexpr (!PAIR) {
+      compute(L, f, acc, dq, ones);
+    } else {
+      // X of activation row col in every register: the ones operand as A,
+      // the activation fragment (row col, this lane's k) as B
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const f32x4 xt = Num<Tag>::mma(ones, f.x[mt][1], Num<Tag>::mma(ones, f.x[mt][0], zero4()));
+        z.ax[mt] = mine ? xt[0] : z.ax[mt];
+      }
+      u32x4 xa[MT][2];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) xa[mt][j] = BITS == 4 ? kperm_x(f.x[mt][j]) : f.x[mt][j];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        u32x4 b0, b1;
+        if constexpr (BITS == 4) {
+          b0 = dequant_word4_kperm<Tag>(f.w[t][0], dq);
+          b1 = dequant_word4_kperm<Tag>(f.w[t][1], dq);
+        } else {
+          b0 = dequant_word8<Tag>(f.w[t][0], f.w[t][1], dq);
+          b1 = dequant_word8<Tag>(f.w[t][2], f.w[t][3], dq);
+        }
+        const float s = half_of(f.sv[t], TSB ? 0x01000c0cu : L.hsel);
+        const float bq = __builtin_fmaf(-OFFQ, s, half_of(f.bv[t], TSB ? 0x03020c0cu : L.hsel));
+        z.bb[t] = mine ? bq : z.bb[t];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const f32x4 p = Num<Tag>::mma(xa[mt][1], b1, Num<Tag>::mma(xa[mt][0], b0, zero4()));
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[t][mt][r] = __builtin_fmaf(s, p[r], acc[t][mt][r]);
+        }
+      }
+    }
+  }
+
   // Barrier once this wavefront has at most n whole steps of loads
   // outstanding (n <= 3).  The scale window precedes every step's loads, so
   // it has landed by the first wait.
@@ -535,9 +606,11 @@ struct Stream {
 
   // iteration c: step c+1 must be in LDS (steps c+2 .. c+DEPTH-1 may still
   // be in flight); step c is in `cur`.
-  __device__ static inline void step(const Ctx& cx, const Lane& L, int c, int c1, int stage,
-                                     int g0w, Frag& cur, Frag& nxt, f32x4 (&acc)[NT][MT],
-                                     const DqConst& dq, const u32x4 ones) {
+  template <bool BM>
+  __device__ static inline void step(const Ctx& cx, const Lane& L, int c, int c0, int c1,
+                                     int stage, int g0w, Frag& cur, Frag& nxt,
+                                     f32x4 (&acc)[NT][MT], const DqConst& dq, const u32x4 ones,
+                                     Bias& z) {
     if (c + 1 < c1) {
       wait_steps(min(DEPTH - 2, c1 - c - 2));
       if (c + DEPTH < c1)
@@ -550,12 +623,23 @@ struct Stream {
     // anything reuses the stages.
     const int st1 = stage == DEPTH - 1 ? 0 : stage + 1;
     read_frag(cx, L, c + 1, st1, g0w, nxt);
-    compute(L, cur, acc, dq, ones);
+    if constexpr (BM) {
+      const int slot = (c - c0) & 3;  // batch slot of this step's bias terms
+      compute_b(L, cur, acc, dq, ones, z, (cx.lane >> 4) == slot);
+      if (slot == 3 || c + 1 == c1) bias_flush(z, acc);
+    } else {
+      compute(L, cur, acc, dq, ones);
+    }
   }
 
   // Accumulate steps [c0, c1) (c1 > c0) of this workgroup into acc.  Every
   // wavefront of the workgroup calls this with the same range (it contains
-  // barriers).  The range covers at most MAX_GROUPS groups.
+  // barriers).  The range covers at most MAX_GROUPS groups.  BM: bias terms
+  // batched into fp32 MFMAs (compute_b); measured on MI355X faster for the
+  // lm_head's long ranges (20 steps per workgroup: 104.6 -> 98.0 us) and
+  // slower for the 27B-class sweep's split ranges and the MoE units, which
+  // keep the per-step FMAs.
+  template <bool BM = false>
   __device__ static inline void run(const Ctx& cx, int c0, int c1, f32x4 (&acc)[NT][MT]) {
     const DqConst dq = dq_const<Tag>();
     const u32x4 ones = ones_operand();
@@ -571,14 +655,16 @@ struct Stream {
     wait_steps(min(DEPTH - 1, c1 - c0 - 1));
     Frag fa, fb;
     read_frag(cx, L, c0, 0, g0w, fa);
+    Bias z;
+    bias_zero(z);
     int c = c0, stage = 0;
     for (; c + 1 < c1; c += 2) {
-      step(cx, L, c, c1, stage, g0w, fa, fb, acc, dq, ones);
+      step<BM>(cx, L, c, c0, c1, stage, g0w, fa, fb, acc, dq, ones, z);
       stage = stage == DEPTH - 1 ? 0 : stage + 1;
-      step(cx, L, c + 1, c1, stage, g0w, fb, fa, acc, dq, ones);
+      step<BM>(cx, L, c + 1, c0, c1, stage, g0w, fb, fa, acc, dq, ones, z);
       stage = stage == DEPTH - 1 ? 0 : stage + 1;
     }
-    if (c < c1) step(cx, L, c, c1, stage, g0w, fa, fb, acc, dq, ones);
+    if (c < c1) step<BM>(cx, L, c, c0, c1, stage, g0w, fa, fb, acc, dq, ones, z);
   }
 };
 
