@@ -541,7 +541,8 @@ def run_moe(args, torch):
     del g
 
     # each gather kernel's launches replayed alone (the gate/up SwiGLU pair
-    # dominates: two thirds of the weight bytes)
+    # dominates: two thirds of the weight bytes); both are moe_stream_kernel
+    # (pair tables), the SwiGLU and the plain instantiation
     hs = [gather_swiglu(x, gate, up, rhs, lhs_indices=lhs, group_size=64)
           for (gate, up, down, rhs, lhs, inv, sc, x, _) in lay]
 
@@ -555,8 +556,8 @@ def run_moe(args, torch):
 
     reps = max(3, args.steps // 4)
     per_kernel = {}
-    for name, f, nbytes in (("gather_persist_kernel", fn_sw, sw_bytes),
-                            ("gather_kernel", fn_dn, dn_bytes)):
+    for name, f, nbytes in (("moe_stream_kernel<swiglu>", fn_sw, sw_bytes),
+                            ("moe_stream_kernel<down>", fn_dn, dn_bytes)):
         gk = graph_of(torch, f)
         kms = time_replays(torch, gk, reps)
         del gk
@@ -564,9 +565,9 @@ def run_moe(args, torch):
                             "us_per_launch": round(kms * 1e3 / layers, 3),
                             "bytes_per_launch": nbytes // layers,
                             "GBps": round(nbytes / (kms * 1e-3) / 1e9, 2)}
-    dom = per_kernel["gather_persist_kernel"]
+    dom = per_kernel["moe_stream_kernel<swiglu>"]
     # algorithmic FLOP of the gate/up launch: T·k routed rows x (gate + up)
-    roofline = roofline_of("moe", "gather_persist_kernel", dom["bytes_per_launch"],
+    roofline = roofline_of("moe", "moe_stream_kernel<swiglu>", dom["bytes_per_launch"],
                            dom["us_per_launch"], 2 * T * k * D * I * 2, per_kernel)
     config = {"workload": "MoE 40 layers, 16 tokens top-8 of 256 experts, hidden 2048, "
                           "expert width 512, int4 gs64", "algorithmic_bytes_per_step": total}
