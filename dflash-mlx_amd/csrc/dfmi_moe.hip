@@ -1238,36 +1238,56 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* y, const i
 }
 
 // The same sums for D % 8 == 0: a lane takes 8 consecutive columns (one
-// 16-byte load per pair, the pair's row id and score read once per
-// wavefront), one wavefront per 512 columns of a token.  Same fma order.
+// 16-byte load per pair), one wavefront per 512 columns of a token.  Same fma
+// order.  Eight pairs at a time, in two memory round trips: lanes 0..7 load
+// the eight pair ids and scores (one vector load each, broadcast with
+// readlane), then every lane requests its eight rows before the first fma (an
+// out-of-range id loads row 0 and is replaced by NaN after the load).  Lanes
+// past D load columns 0..7 and store nothing, so every lane takes part in the
+// broadcast.
 template <typename Tag>
 __global__ __launch_bounds__(64) void combine8_kernel(const uint16_t* y, const int32_t* y_rows,
                                                       const float* scores, uint16_t* out, int T,
                                                       int k, int D) {
   const int t = blockIdx.y;
-  const int d0 = (blockIdx.x * 64 + (int)threadIdx.x) * 8;
-  if (d0 >= D) return;
+  const int lane = (int)threadIdx.x;
+  const int d0 = (blockIdx.x * 64 + lane) * 8;
+  const bool in = d0 < D;
+  const int dl = in ? d0 : 0;  // the column this lane loads
   const int64_t P = (int64_t)T * k;
+  const int64_t base = (int64_t)t * k;
+  const u32x4 nan4 = {0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu};  // NaN in both dtypes
   float acc[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = 0.f;
-#pragma unroll 8
-  for (int j = 0; j < k; ++j) {
-    const int64_t p = (int64_t)t * k + j;
-    const int64_t r = y_rows ? (int64_t)y_rows[p] : p;
-    const float sc = scores[p];
-    u32x4 v;
-    if (r >= 0 && r < P) {
-      v = *reinterpret_cast<const u32x4*>(y + r * D + d0);
-    } else {
-      v = u32x4{0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu};  // NaN in both dtypes
+  for (int j0 = 0; j0 < k; j0 += 8) {
+    const int64_t pl = base + min(j0 + (lane & 7), k - 1);  // slots past k: loaded, not used
+    const int32_t my_id = y_rows ? y_rows[pl] : (int32_t)pl;
+    const float my_sc = scores[pl];
+    u32x4 v[8];
+    float sc[8];
+    bool ok[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int64_t r = __builtin_amdgcn_readlane(my_id, i);
+      sc[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_sc), i));
+      ok[i] = r >= 0 && r < P;
+      v[i] = *reinterpret_cast<const u32x4*>(y + (ok[i] ? r : 0) * D + dl);
     }
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      acc[2 * e] = __builtin_fmaf(sc, Num<Tag>::h2f((uint16_t)(v[e] & 0xFFFFu)), acc[2 * e]);
-      acc[2 * e + 1] = __builtin_fmaf(sc, Num<Tag>::h2f((uint16_t)(v[e] >> 16)), acc[2 * e + 1]);
+    for (int i = 0; i < 8; ++i) {  // a slot past k leaves acc as it is (a select, no branch)
+      const bool use = j0 + i < k;
+      const u32x4 w = ok[i] ? v[i] : nan4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float lo = __builtin_fmaf(sc[i], Num<Tag>::h2f((uint16_t)(w[e] & 0xFFFFu)), acc[2 * e]);
+        const float hi = __builtin_fmaf(sc[i], Num<Tag>::h2f((uint16_t)(w[e] >> 16)), acc[2 * e + 1]);
+        acc[2 * e] = use ? lo : acc[2 * e];
+        acc[2 * e + 1] = use ? hi : acc[2 * e + 1];
+      }
     }
   }
+  if (!in) return;
   u32x4 o;
 #pragma unroll
   for (int e = 0; e < 4; ++e)

@@ -160,7 +160,8 @@ def test_switch_glu_matches_oracle(dev, T, k, E, D, I):
     _check(from_dev(y, "bf16"), oracle.to_f32(y_want, "bf16"), "bf16")
 
 
-@pytest.mark.parametrize("T,k,D", [(16, 8, 2048), (3, 2, 100), (1, 1, 7)])
+@pytest.mark.parametrize("T,k,D", [(16, 8, 2048), (3, 2, 100), (1, 1, 7), (4, 10, 2048),
+                                   (2, 3, 16)])
 def test_moe_combine(dev, T, k, D):
     import torch
 
@@ -177,7 +178,7 @@ def test_moe_combine(dev, T, k, D):
     assert (diff == 0).mean() > 0.99
 
 
-@pytest.mark.parametrize("T,k,D", [(16, 8, 2048), (3, 2, 100)])
+@pytest.mark.parametrize("T,k,D", [(16, 8, 2048), (3, 2, 100), (4, 10, 520)])
 def test_moe_combine_unsort(dev, T, k, D):
     """y handed over in a permuted (expert-sorted) order with y_rows = the
     inverse permutation gives the same bits as the combine over y in pair
