@@ -107,8 +107,8 @@ def workspace(device: torch.device, nbytes: int, kind: str = "qmm") -> tuple[int
 
 def pair_shape(M: int, K: int, N: int, group_size: int, bits: int) -> bool:
     """Shapes whose streaming plan can take a pair table (``dfmi_qmm_affine_pairs``):
-    4-bit, gs 64 / 128, M <= 16, whole 256-k steps (mirrors the library's rule)."""
-    return (int(bits) == 4 and int(group_size) in (64, 128) and 1 <= int(M) <= 16
+    4-bit, gs 64 / 128, M <= 32, whole 256-k steps (mirrors the library's rule)."""
+    return (int(bits) == 4 and int(group_size) in (64, 128) and 1 <= int(M) <= 32
             and int(K) % 256 == 0 and int(K) % (8 * int(group_size)) == 0
             and (int(N) + 63) // 64 <= 16384)
 

@@ -348,11 +348,12 @@ constexpr int kCUs = 256;  // MI355X compute units
 // is a whole number of them
 constexpr bool kAutoRows128 = true;
 
-// Shapes with a pair-streaming plan: 4-bit, gs 64 / 128, one activation
-// block, whole 256-k steps (and a split's K range within the window of the
-// kernel that runs the same plan without pair tables).
+// Shapes with a pair-streaming plan: 4-bit, gs 64 / 128, one or two
+// activation blocks (M <= 32), whole 256-k steps (and a split's K range
+// within the window of the kernel that runs the same plan without pair
+// tables).
 static bool tsb_shape(int64_t M, int64_t K, int64_t N, int gs, int bits) {
-  return bits == 4 && (gs == 64 || gs == 128) && M >= 1 && M <= 16 && K % 256 == 0 &&
+  return bits == 4 && (gs == 64 || gs == 128) && M >= 1 && M <= 32 && K % 256 == 0 &&
          K % (8 * gs) == 0 && (N + kStreamRows - 1) / kStreamRows <= kMaxCounters;
 }
 
@@ -392,10 +393,10 @@ static StreamGeo geo_of(const int64_t* Ns, int nseg) {
 // The same plan (in 64-row blocks: each 128-row block as two) runs on the
 // window kernel when no pair tables are given (80 KB workgroups, two per
 // CU), so both give bit-identical results.
-static void plan_tsb(int64_t K, const StreamGeo& geo, int gs, int rw, int kp_force,
+static void plan_tsb(int64_t K, const StreamGeo& geo, int gs, int rw, int kp_force, int mt,
                      StreamPlan& p) {
   p.bits = 4;
-  p.MT = 1;
+  p.MT = mt;
   p.rw = rw;
   p.WV = 4 * rw;
   p.tsb = 1;
@@ -426,6 +427,11 @@ static void plan_tsb(int64_t K, const StreamGeo& geo, int gs, int rw, int kp_for
   } else if (nb < kCUs) {
     const int kp = std::max(1, kCUs / nb);
     p.kp = std::max(kmin, std::min(kp, std::max(1, p.chunks / 2)));
+    // two activation blocks (two stages, one in flight): raise the split
+    // toward two workgroups per CU while every split keeps >= 8 steps
+    // (27B-class down projection at M = 32: 6 splits 23.5 us vs 3 splits
+    // 25.7 us; o: 3 splits 12.0 us, 6 splits 12.7 us)
+    if (mt == 2) p.kp = std::max(p.kp, std::min(2 * kCUs / nb, p.chunks / 8));
   }
   p.xcd_map = ((nb - p.whole) % 8 == 0) ? 1 : 0;
 }
@@ -471,7 +477,8 @@ static int plan_stream(int64_t M, int64_t K, int64_t N, int gs, int bits,
   }
   const bool waves = tune && tune->waves_per_block > 0;
   const bool tsb = tsb_shape(M, K, N, gs, bits);
-  if (rows == 128 && (!tsb || !geo.nb128 || waves)) {
+  const int mt = M <= 16 ? 1 : 2;  // activation blocks of 16 rows
+  if (rows == 128 && (!tsb || !geo.nb128 || waves || mt == 2)) {
     set_error("dfmi_qmm: 128-row blocks need a pair-streaming shape (4-bit, gs 64 / 128, "
               "M <= 16, K %% 256 == 0, every N a multiple of 128) and automatic wavefronts");
     return DFMI_EINVAL;
@@ -483,14 +490,16 @@ static int plan_stream(int64_t M, int64_t K, int64_t N, int gs, int bits,
     // ranges -- 5120 x 34816 24.5 vs 26.7 us, 17408 x 5120 15.6 vs 17.2 us,
     // 5120 x 151936 95.5 vs 102.7 us -- and loses on short ones: 5120 x
     // 5120 9.6 vs 9.0 us, 4096 x 4096 8.7 vs 7.9 us)
+    // (two activation blocks: 64-row blocks only, two stages of 25 KB, three
+    // workgroups per CU)
     int rw = rows == 128 ? 2 : 1;
-    if (rows == 0 && geo.nb128 && kAutoRows128) {
+    if (rows == 0 && geo.nb128 && kAutoRows128 && mt == 1) {
       StreamPlan q;
-      plan_tsb(K, geo, gs, 2, kp_force, q);
+      plan_tsb(K, geo, gs, 2, kp_force, 1, q);
       const int grid = q.whole + (q.n_blocks - q.whole) * q.kp;
       if ((int64_t)q.n_blocks * q.chunks >= 8ll * grid) rw = 2;
     }
-    plan_tsb(K, geo, gs, rw, kp_force, p);
+    plan_tsb(K, geo, gs, rw, kp_force, mt, p);
     p.grid_x = p.whole + (p.n_blocks - p.whole) * p.kp;
     p.ws_bytes = p.kp > 1 ? kCounterBytes + (size_t)p.kp * (size_t)M *
                                                  (size_t)(p.n_blocks - p.whole) *
@@ -559,7 +568,7 @@ static int plan_stream(int64_t M, int64_t K, int64_t N, int gs, int bits,
   }
   p.grid_x = p.whole + (p.n_blocks - p.whole) * p.kp;
   // forced plans of pair-streaming shapes may still run the pair kernel
-  p.tsb = (tsb_shape(M, K, N, gs, bits) && p.WV == 4 && p.MT == 1) ? 1 : 0;
+  p.tsb = (tsb_shape(M, K, N, gs, bits) && p.WV == 4) ? 1 : 0;
   p.ws_bytes = p.kp > 1 ? kCounterBytes + (size_t)p.kp * (size_t)M *
                                                (size_t)(p.n_blocks - p.whole) * kStreamRows * 4u
                         : 0;
@@ -633,7 +642,9 @@ static void launch_stream_t(const StreamPlan& p, hipStream_t st, const StreamArg
       launch_stream_k<Tag, GS, MT, 8, BITS, true, 2>(p, st, a, m);
       return;
     }
-    if (p.tsb && p.rw == 1 && WV == 4 && segs_have_pairs(m)) {
+  }
+  if constexpr (BITS == 4 && GS >= 64 && WV == 4) {
+    if (p.tsb && p.rw == 1 && segs_have_pairs(m)) {
       launch_stream_k<Tag, GS, MT, WV, BITS, true, 1>(p, st, a, m);
       return;
     }

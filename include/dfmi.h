@@ -116,7 +116,7 @@ size_t dfmi_qmm_workspace_bytes(int64_t M, int64_t K, int64_t N, int group_size,
  * verify_linear.py:166-175, 190-211, 223-232); the reference's
  * VerifyQuantizedLinear likewise precomputes per-module launch state
  * (verify_linear.py:118-223).  With the table, 4-bit gs 64 / 128 calls with
- * M <= 16 and whole 256-k steps stream the pairs with every step instead of
+ * M <= 32 and whole 256-k steps stream the pairs with every step instead of
  * holding a scale / bias window in LDS, so three workgroups share a CU.  The
  * launch plan does not depend on sb_pairs: the result is bit-identical to
  * dfmi_qmm_affine_ex (tuning included) on the same inputs; sb_pairs may be

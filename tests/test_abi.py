@@ -208,13 +208,14 @@ def test_streaming_split_plans(lib):
     assert _plan(lib, 16, 5120, [17408, 17408], gs=128)[4:] == (1, 128)
     assert _plan(lib, 16, 5120, [5120], gs=128)[4:] == (1, 64)
     assert _plan(lib, 16, 5120, [5120], gs=32)[4:] == (0, 64)
-    # M = 17..32, 4-bit: two activation blocks, two workgroups per CU,
-    # splits toward 512 workgroups while each keeps >= 8 steps of 256 k;
-    # whole rounds of 512 then a split tail
-    assert _plan(lib, 32, 17408, [5120])[:2] == (4, 6)
-    assert _plan(lib, 32, 5120, [5120])[:2] == (4, 3)
-    assert _plan(lib, 32, 5120, [17408])[:2] == (4, 1)
-    assert _plan(lib, 32, 5120, [34816])[:3] == (4, 16, 512)
+    # M = 17..32, 4-bit gs 64: pair streaming with two activation blocks in
+    # 64-row blocks (two stages, three workgroups per CU), the M = 16 rules,
+    # and for fewer blocks than CUs splits toward two workgroups per CU while
+    # each keeps >= 8 steps of 256 k
+    assert _plan(lib, 32, 17408, [5120]) == (4, 6, 0, 480, 1, 64)
+    assert _plan(lib, 32, 5120, [5120]) == (4, 3, 0, 240, 1, 64)
+    assert _plan(lib, 32, 5120, [17408])[:3] == (4, 20, 256)
+    assert _plan(lib, 32, 5120, [34816]) == (4, 8, 512, 512 + 32 * 8, 1, 64)
     # 8-bit, M = 16: the unsplit 192-block grid runs as 4 wavefronts, 2 splits
     assert _plan(lib, 16, 4096, [12288], bits=8)[:2] == (4, 2)
     assert _plan(lib, 16, 4096, [4096], bits=8)[:2] == (8, 4)

@@ -105,7 +105,13 @@ def test_sb_pairs_layout(dev, N, G, dtype):
     (8, 12288, 4096, 64),
     (1, 2048, 1000, 128),
     (4, 5120, 5120, 128),
-    (12, 4096, 12288, 64)])
+    (12, 4096, 12288, 64),
+    # two activation blocks (M = 17..32)
+    (32, 5120, 5120, 64),        # 80 blocks: 3 splits
+    (32, 17408, 5120, 64),       # 68 steps: 6 splits, two per CU
+    (24, 5120, 7168, 64),        # q/k/v rows: 2 splits
+    (32, 5120, 34816, 64),       # 544 blocks: 512 whole + 32 x 8 pieces
+    (17, 2048, 64 * 70 - 13, 128)])  # ragged N, gs 128
 @pytest.mark.parametrize("dtype", ["bf16", "f16"])
 def test_pairs_bit_identical_automatic_plans(dev, M, K, N, gs, dtype):
     host, (xt, wt, st, bt) = _case(dev, M, K, N, gs, dtype, seed=M * 7 + K + N)
