@@ -285,7 +285,10 @@ def launch_bytes(M, x, mats, bits):
                            for (w, _, _) in mats)
 
 
-def run_sweep(args, torch, sweep, M, name, with_cpu=True, fuse=True):
+def run_sweep(args, torch, sweep, M, name, with_cpu=True, fuse=True, eager=None):
+    """One sweep line.  eager: time the launches as the modules make them (one
+    Python call per launch on a side stream) instead of graph replays of the
+    same launches; None = the --no-graph flag."""
     from dflash_mlx_amd import _lib, _runtime
     from dflash_mlx_amd.verify_qmm import qmm_launch, qmm_multi_launch
 
@@ -318,7 +321,9 @@ def run_sweep(args, torch, sweep, M, name, with_cpu=True, fuse=True):
                     qmm_multi_launch(x, mats, 64, bits, outs=ys)
         return fn
 
-    if args.no_graph:
+    eager = args.no_graph if eager is None else eager
+    graph_ms = None
+    if eager:
         stream = torch.cuda.Stream()
         step = launches(calls)
         with torch.cuda.stream(stream):
@@ -334,11 +339,16 @@ def run_sweep(args, torch, sweep, M, name, with_cpu=True, fuse=True):
         e1.record(stream)
         torch.cuda.synchronize()
         ms = e0.elapsed_time(e1) / args.steps
+        # the same launches as graph replays, reported beside the line
+        g = graph_of(torch, launches(calls))
+        graph_ms = time_replays(torch, g, args.steps, warmup=args.warmup)
+        del g
     else:
         g = graph_of(torch, launches(calls))
         ms = time_replays(torch, g, args.steps, warmup=args.warmup)
         del g
-    log(f"{name}: {ms:.3f} ms/step ({len(calls)} launches)")
+    log(f"{name}: {ms:.3f} ms/step ({len(calls)} launches"
+        f"{', eager' if eager else ', graph replays'})")
     gbs = step_bytes / (ms * 1e-3) / 1e9
 
     # each kernel's launches replayed alone
@@ -376,10 +386,13 @@ def run_sweep(args, torch, sweep, M, name, with_cpu=True, fuse=True):
     config = {"workload": f"{'27b' if sweep.big else '9b'}-class dense verify-linear sweep",
               "layers": sweep.layers, "linears_per_layer": len(sweep.shapes), "M": M,
               "group_size": 64, "bits": bits,
-              "launch": ("eager" if args.no_graph else "hip-graph") +
+              "launch": ("eager (the modules' launch helpers, one Python call per launch)"
+                         if eager else "hip-graph") +
                         (", q/k/v and gate/up each one shared-activation launch" if fuse
                          else ", one launch per matmul"),
               "launches_per_step": len(calls), "algorithmic_bytes_per_step": step_bytes}
+    if graph_ms is not None:
+        config["graph_replay_ms_per_step"] = round(graph_ms, 4)
     cpu = None
     if with_cpu and not args.no_cpu and bits == 4:
         layer0 = [(x, w_q, s, b) for (x, mats, _) in calls[:len(calls) // sweep.layers]
@@ -714,7 +727,10 @@ def main():
     ap.add_argument("--path", type=int, default=0, help="1 general kernel, 2 streaming kernel")
     ap.add_argument("--tiles", type=int, default=0)
     ap.add_argument("--splits", type=int, default=0)
-    ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="sweeps: time eager launches (the default for the 27B M=16 line)")
+    ap.add_argument("--graph", action="store_true",
+                    help="27B M=16 line: time graph replays instead of eager launches")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-fuse", action="store_true",
                     help="sweeps: one launch per matmul (no shared-activation launches)")
@@ -733,8 +749,13 @@ def main():
     wl = args.workload
     if wl in ("27b", "9b"):
         sweep = Sweep(torch, wl == "27b", args.bits)
+        # the 27B M=16 line is timed as the modules launch (eager; its ~15 us
+        # launches keep the GPU ahead of the host), with the graph replays of
+        # the same launches reported beside it; the other sweeps as graph
+        # replays (the 9B sweep's ~7 us launches would time the host)
+        eager = args.no_graph or (wl == "27b" and args.m == 16 and not args.graph)
         res = headline(args, run_sweep(args, torch, sweep, args.m, f"{wl} M={args.m}",
-                                       fuse=not args.no_fuse))
+                                       fuse=not args.no_fuse, eager=eager))
         default_run = wl == "27b" and args.m == 16 and args.bits == 4 and not args.no_configs \
             and not (args.path or args.tiles or args.splits)
         if default_run:
