@@ -270,8 +270,9 @@ int dfmi_gather_qmm_swiglu(const void *x, int x_dtype, int64_t x_rows,
  * from dflash_mlx/engine/target_qwen_gdn.py:865,874), with the per-layer
  * table built once, as the reference's VerifyQuantizedLinear precomputes
  * per-module state (dflash_mlx/verify_linear.py:118-223).
- * workspace (16-byte aligned, dfmi_gather_workspace_bytes() bytes, zero
- * when first used; the call leaves it zero) lets the units of the last
+ * workspace (16-byte aligned, dfmi_gather_workspace_bytes() bytes: 4 KiB
+ * of counters, zero when first used and left zero by every call, then the
+ * pieces' fp32 partials, which need no clearing) lets the units of the last
  * partial round split along K; NULL runs them whole.  Calls that overlap
  * on one workspace race.
  */
