@@ -285,10 +285,10 @@ def launch_bytes(M, x, mats, bits):
                            for (w, _, _) in mats)
 
 
-def run_sweep(args, torch, sweep, M, name, with_cpu=True, fuse=True, eager=None):
-    """One sweep line.  eager: time the launches as the modules make them (one
-    Python call per launch on a side stream) instead of graph replays of the
-    same launches; None = the --no-graph flag."""
+def run_sweep(args, torch, sweep, M, name, with_cpu=True, fuse=True, also_eager=False):
+    """One sweep line: graph replays of the step's launches (eager launches,
+    one Python call per launch on a side stream, with --no-graph).
+    also_eager: time the eager launches too and report them beside."""
     from dflash_mlx_amd import _lib, _runtime
     from dflash_mlx_amd.verify_qmm import qmm_launch, qmm_multi_launch
 
@@ -321,9 +321,7 @@ def run_sweep(args, torch, sweep, M, name, with_cpu=True, fuse=True, eager=None)
                     qmm_multi_launch(x, mats, 64, bits, outs=ys)
         return fn
 
-    eager = args.no_graph if eager is None else eager
-    graph_ms = None
-    if eager:
+    def eager_ms():
         stream = torch.cuda.Stream()
         step = launches(calls)
         with torch.cuda.stream(stream):
@@ -338,15 +336,18 @@ def run_sweep(args, torch, sweep, M, name, with_cpu=True, fuse=True, eager=None)
                 step()
         e1.record(stream)
         torch.cuda.synchronize()
-        ms = e0.elapsed_time(e1) / args.steps
-        # the same launches as graph replays, reported beside the line
-        g = graph_of(torch, launches(calls))
-        graph_ms = time_replays(torch, g, args.steps, warmup=args.warmup)
-        del g
+        return e0.elapsed_time(e1) / args.steps
+
+    eager = args.no_graph
+    other_ms = None
+    if eager:
+        ms = eager_ms()
     else:
         g = graph_of(torch, launches(calls))
         ms = time_replays(torch, g, args.steps, warmup=args.warmup)
         del g
+        if also_eager:
+            other_ms = eager_ms()
     log(f"{name}: {ms:.3f} ms/step ({len(calls)} launches"
         f"{', eager' if eager else ', graph replays'})")
     gbs = step_bytes / (ms * 1e-3) / 1e9
@@ -391,8 +392,8 @@ def run_sweep(args, torch, sweep, M, name, with_cpu=True, fuse=True, eager=None)
                         (", q/k/v and gate/up each one shared-activation launch" if fuse
                          else ", one launch per matmul"),
               "launches_per_step": len(calls), "algorithmic_bytes_per_step": step_bytes}
-    if graph_ms is not None:
-        config["graph_replay_ms_per_step"] = round(graph_ms, 4)
+    if other_ms is not None:
+        config["eager_ms_per_step"] = round(other_ms, 4)
     cpu = None
     if with_cpu and not args.no_cpu and bits == 4:
         layer0 = [(x, w_q, s, b) for (x, mats, _) in calls[:len(calls) // sweep.layers]
@@ -728,9 +729,7 @@ def main():
     ap.add_argument("--tiles", type=int, default=0)
     ap.add_argument("--splits", type=int, default=0)
     ap.add_argument("--no-graph", action="store_true",
-                    help="sweeps: time eager launches (the default for the 27B M=16 line)")
-    ap.add_argument("--graph", action="store_true",
-                    help="27B M=16 line: time graph replays instead of eager launches")
+                    help="sweeps: time eager launches instead of graph replays")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-fuse", action="store_true",
                     help="sweeps: one launch per matmul (no shared-activation launches)")
@@ -749,13 +748,11 @@ def main():
     wl = args.workload
     if wl in ("27b", "9b"):
         sweep = Sweep(torch, wl == "27b", args.bits)
-        # the 27B M=16 line is timed as the modules launch (eager; its ~15 us
-        # launches keep the GPU ahead of the host), with the graph replays of
-        # the same launches reported beside it; the other sweeps as graph
-        # replays (the 9B sweep's ~7 us launches would time the host)
-        eager = args.no_graph or (wl == "27b" and args.m == 16 and not args.graph)
+        # graph replays (how a serving loop launches a captured step); the
+        # 27B M=16 line also times the same launches made eagerly from Python
         res = headline(args, run_sweep(args, torch, sweep, args.m, f"{wl} M={args.m}",
-                                       fuse=not args.no_fuse, eager=eager))
+                                       fuse=not args.no_fuse,
+                                       also_eager=wl == "27b" and args.m == 16))
         default_run = wl == "27b" and args.m == 16 and args.bits == 4 and not args.no_configs \
             and not (args.path or args.tiles or args.splits)
         if default_run:

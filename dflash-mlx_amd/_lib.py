@@ -78,6 +78,9 @@ _SIGNATURES = {
     "dfmi_qmm_noalloc_scratch_bytes": (_size, []),
     "dfmi_qmm_affine_multi": (_int, [_c_void_p, _int, ctypes.POINTER(QmmSegment), _int, _i64,
                                      _i64, _int, _int, _c_void_p, _size, _c_void_p]),
+    "dfmi_qmm_affine_multi_fused": (_int, [_c_void_p, _int, ctypes.POINTER(QmmSegment), _int,
+                                           _c_void_p, _i64, _i64, _int, _int, _c_void_p, _size,
+                                           _c_void_p]),
     "dfmi_qmm_multi_workspace_bytes": (_size, [_i64, _i64, ctypes.POINTER(ctypes.c_int64), _int,
                                                _int, _int]),
     "dfmi_qmm_multi_kernel_name": (ctypes.c_char_p, [_i64, _i64, ctypes.POINTER(ctypes.c_int64),

@@ -193,3 +193,39 @@ class _PairCache:
 
 
 PAIRS = _PairCache()
+
+
+class _FusedPairCache:
+    """Pair tables of sibling matrices side by side (``[K/gs][N0 + N1 (+ N2)]``,
+    the per-matrix tables concatenated along the columns), for
+    ``dfmi_qmm_affine_multi_fused``; built on first use from the tables given,
+    kept while they live, never built during graph capture (the caller then
+    launches with the per-matrix tables: the same sums)."""
+
+    def __init__(self):
+        self._lock = threading.Lock()
+        self._entries: dict[tuple, tuple] = {}
+
+    def _drop(self, key: tuple):
+        with self._lock:
+            self._entries.pop(key, None)
+
+    def get(self, tables) -> Optional[torch.Tensor]:
+        key = tuple(id(t) for t in tables)
+        ver = tuple(t._version for t in tables)
+        with self._lock:
+            ent = self._entries.get(key)
+        if ent is not None:
+            refs, ever, fused = ent
+            if ever == ver and all(r() is t for r, t in zip(refs, tables)):
+                return fused
+        if torch.cuda.is_current_stream_capturing():
+            return None
+        fused = torch.cat(list(tables), dim=1).contiguous()
+        refs = tuple(weakref.ref(t, lambda _r, k=key: self._drop(k)) for t in tables)
+        with self._lock:
+            self._entries[key] = (refs, ver, fused)
+        return fused
+
+
+FUSED_PAIRS = _FusedPairCache()

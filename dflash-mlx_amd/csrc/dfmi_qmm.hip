@@ -179,6 +179,9 @@ struct StreamSeg {
 struct StreamSegs {
   StreamSeg seg[kMaxSeg];
   int nseg;
+  // [K/GS][sum of N] pair table of all the matrices side by side (each
+  // segment's own t then unused), or null: qmm_stream_fused_kernel
+  const uint32_t* fused;
 };
 
 // workgroup L -> (block nb, K split kpi of kpw).  Workgroups [0, whole) take
@@ -216,7 +219,8 @@ __device__ inline void stream_unit_of(int L, int whole, int kp, int xcd_map, int
 // row groups of WV / 2 wavefronts.
 template <typename Tag, int GS, int MT, int WV, int BITS, int SBPC, bool TSB, int RW>
 __device__ __forceinline__ void qmm_stream_body(const StreamArgs& a, const StreamSeg& g, int nb,
-                                                int kpi, int kp) {
+                                                int kpi, int kp, uint32_t tn = 0,
+                                                uint32_t tc = 0) {
   using S = Stream<Tag, GS, MT, WV, SBPC, BITS, RW, TSB>;
   constexpr int kThreads = 64 * WV;
   typename S::Ctx cx;
@@ -224,7 +228,10 @@ __device__ __forceinline__ void qmm_stream_body(const StreamArgs& a, const Strea
   cx.w = buffer_rsrc(g.w, (uint32_t)g.N * (uint32_t)(a.K / 8 * BITS));
   cx.s = buffer_rsrc(g.s, (uint32_t)g.N * (uint32_t)(a.K / GS) * 2u);
   cx.b = buffer_rsrc(g.b, (uint32_t)g.N * (uint32_t)(a.K / GS) * 2u);
-  if constexpr (TSB) cx.t = buffer_rsrc(g.t, (uint32_t)g.N * (uint32_t)(a.K / GS) * 4u);
+  // TSB: g.t is this matrix's [K/GS][N] pair table, or (tn > 0) a table of
+  // tn columns holding it from column tc on
+  if constexpr (TSB)
+    cx.t = buffer_rsrc(g.t, (tn ? tn : (uint32_t)g.N) * (uint32_t)(a.K / GS) * 4u);
   cx.K = a.K;
   cx.M = a.M;
   cx.N = g.N;
@@ -233,6 +240,8 @@ __device__ __forceinline__ void qmm_stream_body(const StreamArgs& a, const Strea
   cx.lane = threadIdx.x & 63;
   cx.wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   cx.dense();
+  cx.tn = tn;
+  cx.tc = tc;
   const int c0 = (int)((int64_t)kpi * a.chunks / kp);
   const int c1 = (int)((int64_t)(kpi + 1) * a.chunks / kp);
   f32x4 acc[S::NT][MT];
@@ -606,8 +615,58 @@ __global__ __launch_bounds__(64 * WV) void qmm_stream_multi_kernel(StreamArgs a,
   qmm_stream_body<Tag, GS, MT, WV, BITS, SBPC, TSB, RW>(a, g, nb, kpi, kpw);
 }
 
-// Every matrix of m carries its pair table.
+// Two or three matrices over the same activations whose pair tables sit side
+// by side in one [K/GS][N0 + N1 + N2] table (pair streaming only).  Every
+// value the workgroup needs before its first DMA is in the first 14 argument
+// dwords, which the hardware preloads into SGPRs: the activations, the
+// table, the weights, and three packed words (M | kp << 6 | xcd_map << 13 |
+// chunks << 16; whole | N2 << 16; N0 | N1 << 16).  The outputs and the
+// split-K workspace are read from the kernel arguments when the epilogue
+// needs them.  (qmm_stream_multi_kernel instead loads its segment table
+// before the first DMA: ~0.6-0.9 us per launch on MI355X.)
+template <typename Tag, int GS, int MT, int WV, int RW>
+__global__ __launch_bounds__(64 * WV) void qmm_stream_fused_kernel(
+    const uint16_t* x, const uint32_t* t, const uint32_t* w0, const uint32_t* w1,
+    const uint32_t* w2, uint32_t p0, uint32_t p1, uint32_t p2, uint16_t* y0, uint16_t* y1,
+    uint16_t* y2, uint32_t* counters, float* partials, int pstride) {
+  constexpr int NB = kStreamRows * RW;
+  const int M = (int)(p0 & 63u), kp = (int)((p0 >> 6) & 127u), xcd_map = (int)((p0 >> 13) & 1u);
+  const int chunks = (int)(p0 >> 16);
+  const int whole = (int)(p1 & 0xFFFFu), N2 = (int)(p1 >> 16);
+  const int N0 = (int)(p2 & 0xFFFFu), N1 = (int)(p2 >> 16);
+  const int b1 = (N0 + NB - 1) / NB, b2 = b1 + (N1 + NB - 1) / NB;
+  const int n_blocks = b2 + (N2 + NB - 1) / NB;
+  int nb, kpi, kpw;
+  stream_unit_of(blockIdx.x, whole, kp, xcd_map, nb, kpi, kpw);
+  if (nb >= n_blocks) return;  // uniform, before any barrier
+  const bool in1 = nb >= b1, in2 = nb >= b2;  // segment 1 / 2 (uniform)
+  StreamSeg g;
+  g.w = in2 ? w2 : (in1 ? w1 : w0);
+  g.s = nullptr;  // pair streaming: no scale / bias window
+  g.b = nullptr;
+  g.y = in2 ? y2 : (in1 ? y1 : y0);
+  g.N = in2 ? N2 : (in1 ? N1 : N0);
+  g.blk0 = in2 ? b2 : (in1 ? b1 : 0);
+  g.t = t;
+  const uint32_t tc = in2 ? (uint32_t)(N0 + N1) : (in1 ? (uint32_t)N0 : 0u);
+  qmm_stream_body<Tag, GS, MT, WV, 4, kSbPieces, true, RW>(
+      StreamArgs{x, partials, counters, M, chunks * 256, chunks, kp, n_blocks, xcd_map, pstride,
+                 whole},
+      g, nb, kpi, kpw, (uint32_t)(N0 + N1 + N2), tc);
+}
+
+// The fused kernel takes the launch: two or three matrices, each N < 2^16,
+// and the plan's values fit their packed fields.
+static bool fused_fits(const StreamSegs& m, int whole, int kp, int chunks, int M) {
+  if (!m.fused || m.nseg < 2 || m.nseg > 3) return false;
+  for (int i = 0; i < m.nseg; ++i)
+    if (m.seg[i].N >= 65536) return false;
+  return whole < 65536 && kp < 128 && chunks < 65536 && M < 64;
+}
+
+// Every matrix of m carries its pair table (or they share a fused one).
 static bool segs_have_pairs(const StreamSegs& m) {
+  if (m.fused) return true;
   for (int i = 0; i < m.nseg; ++i)
     if (m.seg[i].N > 0 && !m.seg[i].t) return false;
   return true;
@@ -624,6 +683,20 @@ static void launch_stream_k(const StreamPlan& p, hipStream_t st, const StreamArg
                        dim3(64 * WV), lds, st, a.x, g.w, g.s, g.b, g.t, g.y, a.partials,
                        a.counters, a.M, a.K, g.N, a.chunks, a.kp, a.n_blocks, a.xcd_map, a.whole);
   } else {
+    if constexpr (TSB && BITS == 4 && GS >= 64) {
+      if (m.fused) {  // fused_fits() held when the plan was made
+        const uint32_t p0 = (uint32_t)a.M | ((uint32_t)a.kp << 6) | ((uint32_t)a.xcd_map << 13) |
+                            ((uint32_t)a.chunks << 16);
+        const uint32_t p1 = (uint32_t)a.whole | ((uint32_t)(m.nseg > 2 ? m.seg[2].N : 0) << 16);
+        const uint32_t p2 = (uint32_t)m.seg[0].N | ((uint32_t)m.seg[1].N << 16);
+        hipLaunchKernelGGL((qmm_stream_fused_kernel<Tag, GS, MT, WV, RW>), dim3(p.grid_x),
+                           dim3(64 * WV), lds, st, a.x, m.fused, m.seg[0].w, m.seg[1].w,
+                           m.nseg > 2 ? m.seg[2].w : m.seg[1].w, p0, p1, p2, m.seg[0].y,
+                           m.seg[1].y, m.nseg > 2 ? m.seg[2].y : m.seg[1].y, a.counters,
+                           a.partials, a.pstride);
+        return;
+      }
+    }
     hipLaunchKernelGGL((qmm_stream_multi_kernel<Tag, GS, MT, WV, BITS, SBPC, TSB, RW>),
                        dim3(p.grid_x), dim3(64 * WV), lds, st, a, m);
   }
@@ -803,9 +876,13 @@ static int launch_streaming(const void* x, int x_dtype, const StreamSegs& segs, 
   for (int i = 0; i < segs.nseg; ++i) Ns[i] = segs.seg[i].N;
   const int rc = plan_stream(M, K, n_cols, gs, bits, tuning, p, Ns, segs.nseg);
   if (rc != DFMI_OK) return rc;
-  if (p.rw == 2 && !segs_have_pairs(segs)) plan_as_rows64(p);
+  // a fused pair table only where the fused kernel takes the plan (else the
+  // segments' own tables, or none: the window kernel, the same sums)
+  StreamSegs sg = segs;
+  if (sg.fused && !(p.tsb && fused_fits(sg, p.whole, p.kp, p.chunks, (int)M))) sg.fused = nullptr;
+  if (p.rw == 2 && !segs_have_pairs(sg)) plan_as_rows64(p);
   // each matrix's first block in the launch's block size
-  StreamSegs m = segs;
+  StreamSegs m = sg;
   int blk = 0;
   for (int i = 0; i < m.nseg; ++i) {
     m.seg[i].blk0 = blk;
@@ -1115,9 +1192,11 @@ extern "C" const char* dfmi_qmm_multi_kernel_name(int64_t M, int64_t K, const in
   return nseg == 1 ? "qmm_stream_kernel" : "qmm_stream_multi_kernel";
 }
 
-extern "C" int dfmi_qmm_affine_multi(const void* x, int x_dtype, const dfmi_qmm_segment* segs,
-                                     int nseg, int64_t M, int64_t K, int group_size, int bits,
-                                     void* workspace, size_t workspace_bytes, void* stream) {
+// dfmi_qmm_affine_multi / _multi_fused; fused: the matrices' pair tables side
+// by side ([K/gs][sum of N]), or null.
+static int qmm_multi(const void* x, int x_dtype, const dfmi_qmm_segment* segs, int nseg,
+                     const uint32_t* fused, int64_t M, int64_t K, int group_size, int bits,
+                     void* workspace, size_t workspace_bytes, void* stream) {
   if (!segs || nseg < 1 || nseg > kMaxSeg) {
     set_error("dfmi_qmm_multi: 1..%d segments required (got %d)", kMaxSeg, nseg);
     return DFMI_EINVAL;
@@ -1160,6 +1239,7 @@ extern "C" int dfmi_qmm_affine_multi(const void* x, int x_dtype, const dfmi_qmm_
       blk += (int)((Ns[i] + kStreamRows - 1) / kStreamRows);
     }
     m.nseg = nseg;
+    m.fused = fused;
     return launch_streaming(x, x_dtype, m, M, K, cols, group_size, bits, nullptr, workspace,
                             workspace_bytes, static_cast<hipStream_t>(stream));
   }
@@ -1172,6 +1252,26 @@ extern "C" int dfmi_qmm_affine_multi(const void* x, int x_dtype, const dfmi_qmm_
     if (rc != DFMI_OK) return rc;
   }
   return DFMI_OK;
+}
+
+extern "C" int dfmi_qmm_affine_multi(const void* x, int x_dtype, const dfmi_qmm_segment* segs,
+                                     int nseg, int64_t M, int64_t K, int group_size, int bits,
+                                     void* workspace, size_t workspace_bytes, void* stream) {
+  return qmm_multi(x, x_dtype, segs, nseg, nullptr, M, K, group_size, bits, workspace,
+                   workspace_bytes, stream);
+}
+
+extern "C" int dfmi_qmm_affine_multi_fused(const void* x, int x_dtype,
+                                           const dfmi_qmm_segment* segs, int nseg,
+                                           const uint32_t* sb_pairs, int64_t M, int64_t K,
+                                           int group_size, int bits, void* workspace,
+                                           size_t workspace_bytes, void* stream) {
+  if (sb_pairs && !aligned16(sb_pairs)) {
+    set_error("dfmi_qmm_multi_fused: sb_pairs must be 16-byte aligned");
+    return DFMI_EINVAL;
+  }
+  return qmm_multi(x, x_dtype, segs, nseg, sb_pairs, M, K, group_size, bits, workspace,
+                   workspace_bytes, stream);
 }
 
 // ---------------------------------------------------------------------------

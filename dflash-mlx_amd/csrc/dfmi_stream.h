@@ -222,8 +222,12 @@ struct Stream {
     int n0;      // first weight row of this workgroup (in each weight set)
     int wave, lane;
     uint32_t sb_base;  // LDS offset of this run's scale / bias window (past SB_OFF)
+    // TSB: the pair table's row length in columns (0: N) and this matrix's
+    // first column in it (several matrices' tables side by side)
+    uint32_t tn, tc;
 
-    // Dense defaults: activation rows 0 .. M-1, one weight set.
+    // Dense defaults: activation rows 0 .. M-1, one weight set, its own
+    // pair table.
     __device__ inline void dense() {
       xrows = nullptr;
       xbase = 0;
@@ -232,7 +236,10 @@ struct Stream {
       s2 = s;
       b2 = b;
       sb_base = 0;
+      tn = 0;
+      tc = 0;
     }
+    __device__ inline uint32_t t_stride() const { return tn ? tn : (uint32_t)N; }
   };
 
   // Lane-constant offsets, computed once.
@@ -314,7 +321,7 @@ struct Stream {
       const int grp = o / (4 * NB), row = (o % (4 * NB)) / 4;
       const int n = cx.n0 + row;
       L.tg = (cx.lane < TLANES && n < cx.N)
-                 ? ((uint32_t)grp * (uint32_t)cx.N + (uint32_t)n) * 4u
+                 ? ((uint32_t)grp * cx.t_stride() + cx.tc + (uint32_t)n) * 4u
                  : kNoRow;
       L.tfo = (uint32_t)(((kw * 64 / GS) * NB + 64 * rg + col) * 4);
     } else {
@@ -370,7 +377,7 @@ struct Stream {
   // TSB: step c's pairs (groups c GPC .. c GPC + GPC - 1 of the block's rows)
   __device__ static inline void issue_t(const Ctx& cx, const Lane& L, int c, int stage) {
     if (cx.lane < TLANES)
-      dma16(cx.t, L.tg, (uint32_t)c * (uint32_t)(GPC * 4) * (uint32_t)cx.N,
+      dma16(cx.t, L.tg, (uint32_t)c * (uint32_t)(GPC * 4) * cx.t_stride(),
             dfmi_smem + T_OFF + stage * SBS + cx.wave * TPB);
   }
 

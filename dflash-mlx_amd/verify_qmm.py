@@ -106,17 +106,22 @@ def _kparts_tuning():
     return _tuning(kp) if kp > 0 else None
 
 
-def _pairs_ptr(M: int, K: int, N: int, group_size: int, bits: int, scales, biases,
-               pairs) -> int:
-    """Device pointer of the pair table a launch passes: the given one, else
-    the functional cache's for shapes whose plan can use it (0: none)."""
+def _pairs_of(M: int, K: int, N: int, group_size: int, bits: int, scales, biases,
+              pairs) -> Optional[torch.Tensor]:
+    """The pair table a launch passes: the given one, else the functional
+    cache's for shapes whose plan can use it (None: none)."""
     if pairs is None:
         if not _runtime.pair_shape(M, K, N, group_size, bits):
-            return 0
+            return None
         pairs = _runtime.PAIRS.get(scales, biases)
-        if pairs is None:
-            return 0
-    return pairs.data_ptr()
+    return pairs
+
+
+def _pairs_ptr(M: int, K: int, N: int, group_size: int, bits: int, scales, biases,
+               pairs) -> int:
+    """Device pointer of :func:`_pairs_of`'s table (0: none)."""
+    t = _pairs_of(M, K, N, group_size, bits, scales, biases, pairs)
+    return t.data_ptr() if t is not None else 0
 
 
 def qmm_launch(x2: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
@@ -159,15 +164,27 @@ def qmm_multi_launch(x2: torch.Tensor, mats, group_size: int, bits: int,
     ys = outs if outs is not None else [torch.empty((M, N), dtype=x2.dtype, device=dev)
                                         for N in Ns]
     segs = (_lib.QmmSegment * n)()
+    tables = []
     for i, (m, y) in enumerate(zip(mats, ys)):
         w, sc, bi = m[0], m[1], m[2]
         segs[i].w_q, segs[i].scales, segs[i].biases = w.data_ptr(), sc.data_ptr(), bi.data_ptr()
         segs[i].y, segs[i].N = y.data_ptr(), Ns[i]
-        segs[i].sb_pairs = _pairs_ptr(M, K, Ns[i], group_size, bits, sc, bi,
-                                      m[3] if len(m) > 3 else None)
+        t = _pairs_of(M, K, Ns[i], group_size, bits, sc, bi, m[3] if len(m) > 3 else None)
+        tables.append(t)
+        segs[i].sb_pairs = t.data_ptr() if t is not None else 0
     ns = (ctypes.c_int64 * n)(*Ns)
     need = int(lib.dfmi_qmm_multi_workspace_bytes(M, K, ns, n, int(group_size), int(bits)))
     ws, ws_bytes = _runtime.workspace(dev, need) if need else (0, 0)
+    # two or three matrices with tables: the tables side by side, so that the
+    # fused kernel starts its first loads without reading a segment table
+    fused = (_runtime.FUSED_PAIRS.get(tables)
+             if 2 <= n <= 3 and all(t is not None for t in tables) else None)
+    if fused is not None:
+        status = lib.dfmi_qmm_affine_multi_fused(
+            x2.data_ptr(), _runtime.dtype_code(x2.dtype), segs, n, fused.data_ptr(), M, K,
+            int(group_size), int(bits), ws, ws_bytes, _runtime.stream_ptr(dev))
+        _lib.check(status, "dfmi_qmm_affine_multi_fused")
+        return ys
     status = lib.dfmi_qmm_affine_multi(x2.data_ptr(), _runtime.dtype_code(x2.dtype), segs, n, M,
                                        K, int(group_size), int(bits), ws, ws_bytes,
                                        _runtime.stream_ptr(dev))

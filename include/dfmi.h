@@ -215,6 +215,22 @@ typedef struct dfmi_qmm_segment {
 int dfmi_qmm_affine_multi(const void *x, int x_dtype, const dfmi_qmm_segment *segs, int nseg,
                           int64_t M, int64_t K, int group_size, int bits, void *workspace,
                           size_t workspace_bytes, void *stream);
+/*
+ * dfmi_qmm_affine_multi for two or three matrices whose pair tables are
+ * given side by side: sb_pairs [K/group_size][N_0 + N_1 (+ N_2)] uint32, the
+ * matrices' dfmi_sb_pairs tables concatenated along the columns (built once
+ * per sibling group; 16-byte aligned).  The segments' own sb_pairs are used
+ * only where the launch cannot take the combined table (another count of
+ * matrices, an N of 2^16 or more, a plan without pair streaming).  Same call
+ * sites and the same sums as dfmi_qmm_affine_multi (bit-identical y_i); the
+ * kernel then finds every value its first loads need in the arguments the
+ * hardware preloads into registers, instead of reading a segment table
+ * first.
+ */
+int dfmi_qmm_affine_multi_fused(const void *x, int x_dtype, const dfmi_qmm_segment *segs,
+                                int nseg, const uint32_t *sb_pairs, int64_t M, int64_t K,
+                                int group_size, int bits, void *workspace,
+                                size_t workspace_bytes, void *stream);
 size_t dfmi_qmm_multi_workspace_bytes(int64_t M, int64_t K, const int64_t *Ns, int nseg,
                                       int group_size, int bits);
 /* Host-only plan query (no reference counterpart; for benchmarks and

@@ -123,3 +123,61 @@ def test_multi_closed_form_exact(dev):
     for (w_q, s, b), y in zip(mats, _multi(dev, x, mats, gs)):
         want = oracle.quantized_matmul(x, w_q, s, b, group_size=gs, out_dtype="bf16")
         assert np.array_equal(y, want)
+
+
+@pytest.mark.parametrize("M,K,Ns,gs", [
+    (16, 5120, (5120, 1024, 1024), 64),    # q/k/v rows: 64-row blocks, 2 splits
+    (16, 5120, (17408, 17408), 64),        # gate/up: 128-row blocks, whole + pieces
+    (16, 4096, (4096, 1024, 1024), 128),
+    (32, 5120, (5120, 1024, 1024), 64),    # two activation blocks
+    (8, 2048, (1000, 200, 136), 64),       # ragged N
+    (4, 1024, (512, 512), 64)])
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_fused_pair_table_bit_identical(dev, M, K, Ns, gs, dtype):
+    """dfmi_qmm_affine_multi_fused (the matrices' pair tables side by side)
+    gives the same bits as dfmi_qmm_affine_multi with each matrix's own
+    table, on the same plan; a second call over the same workspace too."""
+    import torch
+
+    from dflash_mlx_amd import _lib, _runtime
+
+    lib = _lib.load()
+    rng_seed = M + K + sum(Ns)
+    cases = [make_qmm_case(M, K, N, gs, dtype=dtype, seed=rng_seed + i) for i, N in enumerate(Ns)]
+    x = to_dev(cases[0][0], dtype, dev)
+    mats = [(to_dev(c[1], "u32", dev), to_dev(c[2], dtype, dev), to_dev(c[3], dtype, dev))
+            for c in cases]
+    tables = [_runtime.build_sb_pairs(s, b) for (_, s, b) in mats]
+    fused = torch.cat(tables, dim=1).contiguous()
+    n = len(Ns)
+    ns = (ctypes.c_int64 * n)(*Ns)
+    need = int(lib.dfmi_qmm_multi_workspace_bytes(M, K, ns, n, gs, 4))
+    ws = torch.zeros(need + 256, dtype=torch.uint8, device=dev)
+    wsp = (ws.data_ptr() + 255) // 256 * 256 if need else 0
+
+    def call(use_fused):
+        ys = [torch.full((M, N), float("nan"), dtype=x.dtype, device=dev) for N in Ns]
+        segs = (_lib.QmmSegment * n)()
+        for i, ((w, s, b), y) in enumerate(zip(mats, ys)):
+            segs[i].w_q, segs[i].scales, segs[i].biases = w.data_ptr(), s.data_ptr(), b.data_ptr()
+            segs[i].y, segs[i].N = y.data_ptr(), Ns[i]
+            segs[i].sb_pairs = 0 if use_fused else tables[i].data_ptr()
+        st = _runtime.stream_ptr(dev)
+        if use_fused:
+            rc = lib.dfmi_qmm_affine_multi_fused(x.data_ptr(), _runtime.dtype_code(x.dtype), segs,
+                                                 n, fused.data_ptr(), M, K, gs, 4, wsp, need, st)
+        else:
+            rc = lib.dfmi_qmm_affine_multi(x.data_ptr(), _runtime.dtype_code(x.dtype), segs, n,
+                                           M, K, gs, 4, wsp, need, st)
+        _lib.check(rc, "multi")
+        torch.cuda.synchronize()
+        return [from_dev(y, dtype) for y in ys]
+
+    want = call(False)
+    for _ in range(2):
+        got = call(True)
+        for g, w in zip(got, want):
+            assert np.array_equal(g, w)
+    for g, c in zip(got, cases):  # every matrix multiplies the shared x (cases[0][0])
+        if g.size <= (1 << 22):
+            _check(g, cases[0][0], c[1], c[2], c[3], gs, dtype)
