@@ -585,17 +585,27 @@ static int plan_stream(int64_t M, int64_t K, int64_t N, int gs, int bits,
 }
 
 // The arguments as scalars, not a by-value struct, so that they are
-// preloaded into SGPRs at wave start (-amdgpu-kernarg-preload-count).
+// preloaded into SGPRs at wave start (-amdgpu-kernarg-preload-count): the
+// hardware preloads 14 dwords on gfx950, so everything the first DMA needs
+// comes first (x, w, t, s, b, a packed word M | xcd_map << 6 | kp << 7 |
+// chunks << 16, N, whole; the block count and K follow from N and chunks)
+// and the outputs and split-K workspace, first needed in the epilogue, last.
+// (With M, K, N ... after the eight pointers a workgroup waited for one
+// scalar-load round trip before its first DMA.)
 template <typename Tag, int GS, int MT, int WV, int BITS, int SBPC, bool TSB, int RW>
 __global__ __launch_bounds__(64 * WV) void qmm_stream_kernel(
-    const uint16_t* x, const uint32_t* w, const uint16_t* s, const uint16_t* b, const uint32_t* t,
-    uint16_t* y, float* partials, uint32_t* counters, int M, int K, int N, int chunks, int kp,
-    int n_blocks, int xcd_map, int whole) {
+    const uint16_t* x, const uint32_t* w, const uint32_t* t, const uint16_t* s,
+    const uint16_t* b, uint32_t p0, int N, int whole, uint16_t* y, float* partials,
+    uint32_t* counters) {
+  using S = Stream<Tag, GS, MT, WV, SBPC, BITS, RW, TSB>;
+  const int M = (int)(p0 & 63u), xcd_map = (int)((p0 >> 6) & 1u), kp = (int)((p0 >> 7) & 511u);
+  const int chunks = (int)(p0 >> 16);
+  const int n_blocks = (N + S::NB - 1) / S::NB;
   int nb, kpi, kpw;
   stream_unit_of(blockIdx.x, whole, kp, xcd_map, nb, kpi, kpw);
   if (nb >= n_blocks) return;  // uniform, before any barrier
   qmm_stream_body<Tag, GS, MT, WV, BITS, SBPC, TSB, RW>(
-      StreamArgs{x, partials, counters, M, K, chunks, kp, n_blocks, xcd_map,
+      StreamArgs{x, partials, counters, M, chunks * S::CK, chunks, kp, n_blocks, xcd_map,
                  kStreamRows * RW * (n_blocks - whole), whole},
       StreamSeg{w, s, b, y, N, 0, t}, nb, kpi, kpw);
 }
@@ -679,9 +689,13 @@ static void launch_stream_k(const StreamPlan& p, hipStream_t st, const StreamArg
   const int lds = Stream<Tag, GS, MT, WV, SBPC, BITS, RW, TSB>::LDS_BYTES;
   if (m.nseg == 1) {
     const StreamSeg& g = m.seg[0];
+    // (the packed fields hold every plan: M <= 32, kp < 512, chunks < 2^16;
+    // launch_streaming checks them)
+    const uint32_t p0 = (uint32_t)a.M | ((uint32_t)a.xcd_map << 6) | ((uint32_t)a.kp << 7) |
+                        ((uint32_t)a.chunks << 16);
     hipLaunchKernelGGL((qmm_stream_kernel<Tag, GS, MT, WV, BITS, SBPC, TSB, RW>), dim3(p.grid_x),
-                       dim3(64 * WV), lds, st, a.x, g.w, g.s, g.b, g.t, g.y, a.partials,
-                       a.counters, a.M, a.K, g.N, a.chunks, a.kp, a.n_blocks, a.xcd_map, a.whole);
+                       dim3(64 * WV), lds, st, a.x, g.w, g.t, g.s, g.b, p0, g.N, a.whole, g.y,
+                       a.partials, a.counters);
   } else {
     if constexpr (TSB && BITS == 4 && GS >= 64) {
       if (m.fused) {  // fused_fits() held when the plan was made
@@ -878,6 +892,11 @@ static int launch_streaming(const void* x, int x_dtype, const StreamSegs& segs, 
   if (rc != DFMI_OK) return rc;
   // a fused pair table only where the fused kernel takes the plan (else the
   // segments' own tables, or none: the window kernel, the same sums)
+  if (M > 63 || p.kp >= 512 || p.chunks >= 65536) {  // the kernels' packed argument fields
+    set_error("dfmi_qmm: plan outside the kernel's argument fields (M %lld, kp %d, steps %d)",
+              (long long)M, p.kp, p.chunks);
+    return DFMI_EINVAL;
+  }
   StreamSegs sg = segs;
   if (sg.fused && !(p.tsb && fused_fits(sg, p.whole, p.kp, p.chunks, (int)M))) sg.fused = nullptr;
   if (p.rw == 2 && !segs_have_pairs(sg)) plan_as_rows64(p);
