@@ -188,7 +188,19 @@ __global__ __launch_bounds__(kMaxWaves * 64) void lmhead_greedy_kernel(LmArgs a)
 // TSB / RW: the pair-streaming main loop with 128-row blocks (two row groups
 // of 4 wavefronts sharing the activation stage); the window loop otherwise.
 template <typename Tag, int GS, int MT, int WV, bool TSB = false, int RW = 1>
-__global__ __launch_bounds__(64 * WV) void lmhead_stream_kernel(LmArgs a) {
+__global__ __launch_bounds__(64 * WV) void lmhead_stream_kernel(
+    const uint16_t* h, const uint32_t* w, const uint32_t* t, const uint16_t* s,
+    const uint16_t* b, int M, int K, int V, const uint8_t* mask, uint16_t* logits,
+    float softcap, int chunks, int n_blocks, unsigned long long* keys, uint32_t* counter,
+    uint32_t* posterior, int32_t* accept_len, uint32_t* bonus, const uint32_t* verify_ids,
+    int out_M) {
+  // Scalar arguments, what the first DMA needs first: the hardware preloads
+  // the first 14 dwords into SGPRs (h, w, t, s, b, M, K, V), so a workgroup
+  // starts its loads without a scalar-load round trip; the rest is first
+  // needed by the epilogue.
+  const LmArgs a{h,    w,     s,    b,   t,        mask,     logits,
+                 softcap, M, K, V, chunks, n_blocks,
+                 GreedyOut{keys, counter, posterior, accept_len, bonus, verify_ids, out_M}};
   using S = Stream<Tag, GS, MT, WV, kSbPieces, 4, RW, TSB>;
   constexpr int kThreads = 64 * WV;
   // Dynamic LDS only (two workgroups of 4 wavefronts fill a CU's LDS): the
@@ -382,7 +394,9 @@ static void launch_lm_stream_t(int blocks, hipStream_t st, const LmArgs& a) {
       hipFuncAttributeMaxDynamicSharedMemorySize, lds);
   (void)attr;
   hipLaunchKernelGGL((lmhead_stream_kernel<Tag, GS, MT, WV, TSB, RW>), dim3(blocks),
-                     dim3(64 * WV), lds, st, a);
+                     dim3(64 * WV), lds, st, a.h, a.w, a.t, a.s, a.b, a.M, a.K, a.V, a.mask,
+                     a.logits, a.softcap, a.chunks, a.n_blocks, a.out.keys, a.out.counter,
+                     a.out.posterior, a.out.accept_len, a.out.bonus, a.out.verify_ids, a.out.M);
 }
 
 // With the pair table (gs 64 / 128, one activation block): 128-row blocks,

@@ -621,8 +621,33 @@ struct MoeLayout {
   static_assert(RUNM % 8 == 0 && NSEG % 4 == 0, "alignment");
 };
 
+// Scalar arguments, what the start needs first: the hardware preloads the
+// first 14 dwords into SGPRs (the pair ids, x, the weights, the pair table,
+// P, K), so a workgroup reads its pair ids without a scalar-load round trip
+// before them; the rest comes from the kernel arguments when first used.
 template <typename Tag, int GS, bool GLU>
-__global__ __launch_bounds__(512) void moe_stream_kernel(GatherArgs a) {
+__global__ __launch_bounds__(512) void moe_stream_kernel(
+    const int32_t* g_lhs, const int32_t* g_rhs, const uint16_t* g_x, const uint32_t* g_w0,
+    const uint32_t* g_w1, const uint32_t* g_t, int g_P, int g_K, int g_N, int g_E,
+    int64_t g_x_rows, uint16_t* g_y, uint32_t* g_wsc, float* g_wsp) {
+  GatherArgs a;
+  a.x = g_x;
+  a.x_rows = g_x_rows;
+  a.w[0] = g_w0;
+  a.w[1] = g_w1;
+  a.s[0] = a.s[1] = nullptr;
+  a.b[0] = a.b[1] = nullptr;
+  a.lhs = g_lhs;
+  a.rhs = g_rhs;
+  a.t = g_t;
+  a.ws_counters = g_wsc;
+  a.ws_partials = g_wsp;
+  a.y = g_y;
+  a.P = g_P;
+  a.K = g_K;
+  a.N = g_N;
+  a.E = g_E;
+  a.chunks = 0;
   using LY = MoeLayout<Tag, GS>;
   using S = typename LY::S;
   constexpr int OUTC = GLU ? 64 : 128;  // output columns per unit
@@ -987,7 +1012,9 @@ static void launch_moe_stream_t(const GatherArgs& a, int grid, hipStream_t st) {
       reinterpret_cast<const void*>(&moe_stream_kernel<Tag, GS, GLU>),
       hipFuncAttributeMaxDynamicSharedMemorySize, LY::BYTES);
   (void)attr;
-  hipLaunchKernelGGL((moe_stream_kernel<Tag, GS, GLU>), dim3(grid), dim3(512), LY::BYTES, st, a);
+  hipLaunchKernelGGL((moe_stream_kernel<Tag, GS, GLU>), dim3(grid), dim3(512), LY::BYTES, st,
+                     a.lhs, a.rhs, a.x, a.w[0], a.w[1], a.t, a.P, a.K, a.N, a.E, a.x_rows, a.y,
+                     a.ws_counters, a.ws_partials);
 }
 
 template <typename Tag, bool GLU>
