@@ -361,6 +361,12 @@ def run_sweep(args, torch, sweep, M, name, with_cpu=True, fuse=True, also_eager=
         if len(mats) > 1:
             ns = (ctypes.c_int64 * len(mats))(*[w.shape[0] for (w, _, _) in mats])
             kname = lib.dfmi_qmm_multi_kernel_name(M, x.shape[1], ns, len(mats), 64, bits)
+            # two or three pair-streaming matrices run with their tables side
+            # by side (verify_qmm.qmm_multi_launch): qmm_stream_fused_kernel
+            if kname == b"qmm_stream_multi_kernel" and 2 <= len(mats) <= 3 and all(
+                    _runtime.pair_shape(M, x.shape[1], w.shape[0], 64, bits)
+                    for (w, _, _) in mats):
+                kname = b"qmm_stream_fused_kernel"
         if kname is None:
             kname = lib.dfmi_qmm_kernel_name(M, x.shape[1], N0, 64, bits, tptr)
         groups.setdefault(kname.decode(), []).append(c)
