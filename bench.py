@@ -256,76 +256,113 @@ class Sweep:
         log(f"{'27b' if big else '9b'} weights ready: {len(self.weights)} matrices, "
             f"{time.time() - t0:.1f} s")
 
-    def launches(self, M, fuse):
-        """The step's launches: ``(x, [(w, s, b)], [y])``.  Unfused, every
-        matmul reads its own activations; fused, q/k/v share one input and
-        gate/up another (as in the model), one launch each."""
-        torch = self.torch
-        groups = [[0, 1, 2], [3], [4, 5], [6]] if fuse else [[i] for i in range(7)]
-        out = []
+    def model(self, fuse):
+        """The sweep's verify linears as a module tree -- layer l's q/k/v/o
+        under ``self_attn`` and gate/up/down under ``mlp``, sharing the weight
+        tensors -- swapped in by ``install_verify_linears`` as the loader does
+        (verify kernels on; q/k/v and gate/up grouped unless ``fuse`` is
+        False) and prewarmed.  Cached per ``fuse``."""
+        cache = self.__dict__.setdefault("_models", {})
+        if fuse in cache:
+            return cache[fuse]
+        from torch import nn
+
+        from dflash_mlx_amd.verify_linear import (QuantizedLinear, install_verify_linears,
+                                                  prewarm_verify_kernels)
+
+        names = [("self_attn", "q_proj"), ("self_attn", "k_proj"), ("self_attn", "v_proj"),
+                 ("self_attn", "o_proj"), ("mlp", "gate_proj"), ("mlp", "up_proj"),
+                 ("mlp", "down_proj")]
+        root = nn.Module()
+        root.layers = nn.ModuleList()
         for l in range(self.layers):
+            layer = nn.Module()
+            layer.self_attn, layer.mlp = nn.Module(), nn.Module()
+            for i, (par, nm) in enumerate(names):
+                w, sc, bi = self.weights[l * len(self.shapes) + i]
+                setattr(getattr(layer, par), nm,
+                        QuantizedLinear(w, sc, bi, group_size=64, bits=self.bits))
+            root.layers.append(layer)
+        n = install_verify_linears(root, enable_qmm=True, fuse_siblings=fuse)
+        assert n == len(self.weights), n
+        prewarm_verify_kernels(root)
+        self.torch.cuda.synchronize()
+        cache[fuse] = root
+        return root
+
+    def drop_models(self):
+        self.__dict__.pop("_models", None)
+
+    def calls(self, root, M):
+        """The step: per layer ``(x, [modules])`` for q/k/v (one input), o,
+        gate/up (one input) and down, each input seeded, as a decoder layer
+        calls them."""
+        torch = self.torch
+        groups = [[0, 1, 2], [3], [4, 5], [6]]
+        out = []
+        for l, layer in enumerate(root.layers):
+            mods = [layer.self_attn.q_proj, layer.self_attn.k_proj, layer.self_attn.v_proj,
+                    layer.self_attn.o_proj, layer.mlp.gate_proj, layer.mlp.up_proj,
+                    layer.mlp.down_proj]
             for grp in groups:
                 i0 = l * len(self.shapes) + grp[0]
-                mats = [self.weights[l * len(self.shapes) + i] for i in grp]
-                K = mats[0][0].shape[1] * 32 // self.bits
+                K = self.shapes[grp[0]][1]
                 xg = torch.Generator(device=self.dev)
                 xg.manual_seed(10000 + i0)
                 x = torch.randn((M, K), generator=xg, device=self.dev).to(torch.bfloat16)
-                ys = [torch.empty((M, w.shape[0]), dtype=torch.bfloat16, device=self.dev)
-                      for (w, _, _) in mats]
-                out.append((x, mats, ys))
+                out.append((x, [mods[i] for i in grp]))
         return out
 
 
-def launch_bytes(M, x, mats, bits):
+def launch_bytes(M, x, mods, bits):
     """Algorithmic bytes of one launch: every matrix's packed weights, scales
     and biases and output rows, the shared activations once."""
     K = x.shape[1]
-    return 2 * M * K + sum(alg_bytes(M, K, w.shape[0], bits=bits) - 2 * M * K
-                           for (w, _, _) in mats)
+    return 2 * M * K + sum(alg_bytes(M, K, m.weight.shape[0], bits=bits) - 2 * M * K
+                           for m in mods)
+
+
+def call_kernel(lib, M, x, mods, bits, fuse):
+    """Name of the kernel a step call launches: the grouped siblings' shared
+    launch (its pair tables side by side: qmm_stream_fused_kernel), or one
+    module's launch."""
+    K = x.shape[1]
+    st = mods[0].__dict__.get("_verify_state")
+    if fuse and len(mods) > 1 and st is not None and st.group is not None:
+        grp = st.group
+        if grp.fused is not None and len(grp.active) == len(grp.states) and 2 <= len(mods) <= 3:
+            return "qmm_stream_fused_kernel"
+        ns = (ctypes.c_int64 * len(mods))(*[m.weight.shape[0] for m in mods])
+        return lib.dfmi_qmm_multi_kernel_name(M, K, ns, len(mods), 64, bits).decode()
+    return lib.dfmi_qmm_kernel_name(M, K, mods[0].weight.shape[0], 64, bits, None).decode()
 
 
 def run_sweep(args, torch, sweep, M, name, with_cpu=True, fuse=True, also_eager=False):
-    """One sweep line: graph replays of the step's launches (eager launches,
-    one Python call per launch on a side stream, with --no-graph).
-    also_eager: time the eager launches too and report them beside."""
-    from dflash_mlx_amd import _lib, _runtime
-    from dflash_mlx_amd.verify_qmm import qmm_launch, qmm_multi_launch
+    """One sweep line: graph replays of the step's module calls (eager calls
+    with --no-graph).  The modules are the drop-in path: installed verify
+    linears, siblings grouped into shared-activation launches unless fuse is
+    False.  also_eager: time the eager calls too and report them beside."""
+    from dflash_mlx_amd import _lib
 
     bits = sweep.bits
-    fuse = fuse and not (args.path or args.tiles or args.splits)
-    calls = sweep.launches(M, fuse)
-    step_bytes = sum(launch_bytes(M, x, mats, bits) for (x, mats, _) in calls)
-    tuning = None
-    if args.path or args.tiles or args.splits:
-        tuning = _lib.QmmTuning(args.path, args.tiles, args.splits, args.splits)
     lib = _lib.load()
-    tptr = ctypes.byref(tuning) if tuning is not None else None
-    need = 0
-    for (x, mats, _) in calls:
-        K = x.shape[1]
-        if len(mats) == 1:
-            need = max(need, lib.dfmi_qmm_workspace_bytes_ex(M, K, mats[0][0].shape[0], 64, bits,
-                                                             tptr))
-        else:
-            ns = (ctypes.c_int64 * len(mats))(*[w.shape[0] for (w, _, _) in mats])
-            need = max(need, lib.dfmi_qmm_multi_workspace_bytes(M, K, ns, len(mats), 64, bits))
+    root = sweep.model(fuse)
+    calls = sweep.calls(root, M)
+    step_bytes = sum(launch_bytes(M, x, mods, bits) if fuse else
+                     sum(launch_bytes(M, x, [m], bits) for m in mods) for (x, mods) in calls)
+    n_launches = len(calls) if fuse else sum(len(mods) for (_, mods) in calls)
 
-    def launches(subset):
+    def step_of(subset):
         def fn():
-            for (x, mats, ys) in subset:
-                if len(mats) == 1:
-                    w_q, s, b = mats[0]
-                    qmm_launch(x, w_q, s, b, w_q.shape[0], 64, bits, tuning, out=ys[0])
-                else:
-                    qmm_multi_launch(x, mats, 64, bits, outs=ys)
+            for (x, mods) in subset:
+                for m in mods:
+                    m(x)
         return fn
 
     def eager_ms():
         stream = torch.cuda.Stream()
-        step = launches(calls)
+        step = step_of(calls)
         with torch.cuda.stream(stream):
-            _runtime.WORKSPACES.reserve(sweep.dev, need)
             for _ in range(args.warmup):
                 step()
         torch.cuda.synchronize()
@@ -343,42 +380,30 @@ def run_sweep(args, torch, sweep, M, name, with_cpu=True, fuse=True, also_eager=
     if eager:
         ms = eager_ms()
     else:
-        g = graph_of(torch, launches(calls))
+        g = graph_of(torch, step_of(calls))
         ms = time_replays(torch, g, args.steps, warmup=args.warmup)
         del g
         if also_eager:
             other_ms = eager_ms()
-    log(f"{name}: {ms:.3f} ms/step ({len(calls)} launches"
+    log(f"{name}: {ms:.3f} ms/step ({n_launches} launches"
         f"{', eager' if eager else ', graph replays'})")
     gbs = step_bytes / (ms * 1e-3) / 1e9
 
     # each kernel's launches replayed alone
     groups = {}
-    for c in calls:
-        x, mats, _ = c
-        N0 = mats[0][0].shape[0]
-        kname = None
-        if len(mats) > 1:
-            ns = (ctypes.c_int64 * len(mats))(*[w.shape[0] for (w, _, _) in mats])
-            kname = lib.dfmi_qmm_multi_kernel_name(M, x.shape[1], ns, len(mats), 64, bits)
-            # two or three pair-streaming matrices run with their tables side
-            # by side (verify_qmm.qmm_multi_launch): qmm_stream_fused_kernel
-            if kname == b"qmm_stream_multi_kernel" and 2 <= len(mats) <= 3 and all(
-                    _runtime.pair_shape(M, x.shape[1], w.shape[0], 64, bits)
-                    for (w, _, _) in mats):
-                kname = b"qmm_stream_fused_kernel"
-        if kname is None:
-            kname = lib.dfmi_qmm_kernel_name(M, x.shape[1], N0, 64, bits, tptr)
-        groups.setdefault(kname.decode(), []).append(c)
+    for (x, mods) in calls:
+        units = [mods] if fuse else [[m] for m in mods]
+        for u in units:
+            groups.setdefault(call_kernel(lib, M, x, u, bits, fuse), []).append((x, u))
     per_kernel = {}
     reps = max(3, args.steps // 4)
     for kname, subset in groups.items():
-        gk = graph_of(torch, launches(subset))
+        gk = graph_of(torch, step_of(subset))
         kms = time_replays(torch, gk, reps)
         del gk
-        kbytes = sum(launch_bytes(M, x, mats, bits) for (x, mats, _) in subset)
-        kflops = sum(2 * M * x.shape[1] * w.shape[0] for (x, mats, _) in subset
-                     for (w, _, _) in mats)
+        kbytes = sum(launch_bytes(M, x, mods, bits) for (x, mods) in subset)
+        kflops = sum(2 * M * x.shape[1] * m.weight.shape[0] for (x, mods) in subset
+                     for m in mods)
         per_kernel[kname] = {"launches_per_step": len(subset), "ms_per_step": round(kms, 4),
                              "us_per_launch": round(kms * 1e3 / len(subset), 3),
                              "bytes_per_launch": kbytes // len(subset),
@@ -393,17 +418,16 @@ def run_sweep(args, torch, sweep, M, name, with_cpu=True, fuse=True, also_eager=
     config = {"workload": f"{'27b' if sweep.big else '9b'}-class dense verify-linear sweep",
               "layers": sweep.layers, "linears_per_layer": len(sweep.shapes), "M": M,
               "group_size": 64, "bits": bits,
-              "launch": ("eager (the modules' launch helpers, one Python call per launch)"
-                         if eager else "hip-graph") +
-                        (", q/k/v and gate/up each one shared-activation launch" if fuse
-                         else ", one launch per matmul"),
-              "launches_per_step": len(calls), "algorithmic_bytes_per_step": step_bytes}
+              "launch": ("eager module calls" if eager else "hip-graph replays of the module calls") +
+                        (" (install_verify_linears default: q/k/v and gate/up each one "
+                         "shared-activation launch)" if fuse
+                         else " (fuse_siblings=False: one launch per matmul)"),
+              "launches_per_step": n_launches, "algorithmic_bytes_per_step": step_bytes}
     if other_ms is not None:
         config["eager_ms_per_step"] = round(other_ms, 4)
     cpu = None
     if with_cpu and not args.no_cpu and bits == 4:
-        layer0 = [(x, w_q, s, b) for (x, mats, _) in calls[:len(calls) // sweep.layers]
-                  for (w_q, s, b) in mats]
+        layer0 = [(x, m.weight, m.scales, m.biases) for (x, mods) in calls[:4] for m in mods]
         cpu = cpu_baseline_calls(torch, layer0, M,
                                  f"layer 0 of the sweep ({len(sweep.shapes)} matmuls, M={M})")
     del calls
@@ -731,14 +755,12 @@ def main():
     ap.add_argument("--m", type=int, default=16)
     ap.add_argument("--bits", type=int, default=4, choices=[4, 8],
                     help="weight bits of the 9b / 27b sweeps")
-    ap.add_argument("--path", type=int, default=0, help="1 general kernel, 2 streaming kernel")
-    ap.add_argument("--tiles", type=int, default=0)
-    ap.add_argument("--splits", type=int, default=0)
     ap.add_argument("--no-graph", action="store_true",
-                    help="sweeps: time eager launches instead of graph replays")
+                    help="sweeps: time eager module calls instead of graph replays")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-fuse", action="store_true",
-                    help="sweeps: one launch per matmul (no shared-activation launches)")
+                    help="sweeps: install_verify_linears(fuse_siblings=False), one launch per "
+                         "matmul")
     ap.add_argument("--no-configs", action="store_true",
                     help="default run: print the 27B line without the other configurations")
     args = ap.parse_args()
@@ -755,18 +777,18 @@ def main():
     if wl in ("27b", "9b"):
         sweep = Sweep(torch, wl == "27b", args.bits)
         # graph replays (how a serving loop launches a captured step); the
-        # 27B M=16 line also times the same launches made eagerly from Python
+        # 27B M=16 line also times the same module calls made eagerly
         res = headline(args, run_sweep(args, torch, sweep, args.m, f"{wl} M={args.m}",
                                        fuse=not args.no_fuse,
                                        also_eager=wl == "27b" and args.m == 16))
-        default_run = wl == "27b" and args.m == 16 and args.bits == 4 and not args.no_configs \
-            and not (args.path or args.tiles or args.splits)
+        default_run = wl == "27b" and args.m == 16 and args.bits == 4 and not args.no_configs
         if default_run:
             configs = {}
-            configs["27b_separate"] = run_sweep(args, torch, sweep, 16, "27b M=16 separate",
-                                                with_cpu=False, fuse=False)
             for M in (8, 32):
                 configs[f"27b_m{M}"] = run_sweep(args, torch, sweep, M, f"27b M={M}")
+            configs["27b_separate"] = run_sweep(args, torch, sweep, 16, "27b M=16 separate",
+                                                with_cpu=False, fuse=False, also_eager=True)
+            sweep.drop_models()
             del sweep
             torch.cuda.empty_cache()
             configs["9b"] = run_sweep(args, torch, Sweep(torch, False, 4), 16, "9b M=16")

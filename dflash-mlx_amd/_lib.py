@@ -21,6 +21,8 @@ DFMI_BF16 = 0
 DFMI_F16 = 1
 DFMI_F32 = 2
 
+DFMI_QMM_RECORD_BYTES = 1024
+
 _c_void_p = ctypes.c_void_p
 _i64 = ctypes.c_int64
 _int = ctypes.c_int
@@ -29,7 +31,7 @@ _float = ctypes.c_float
 
 
 class QmmTuning(ctypes.Structure):
-    """dfmi_qmm_tuning: path (1 general, 2 streaming, 3 persistent), tiles_per_wave,
+    """dfmi_qmm_tuning: path (1 general, 2 streaming), tiles_per_wave,
     waves_per_block (general kernel K split), k_splits (streaming kernel K
     split across workgroups), rows_per_block (streaming kernel, 64 or 128);
     0 = automatic."""
@@ -85,6 +87,9 @@ _SIGNATURES = {
                                                _int, _int]),
     "dfmi_qmm_multi_kernel_name": (ctypes.c_char_p, [_i64, _i64, ctypes.POINTER(ctypes.c_int64),
                                                      _int, _int, _int]),
+    "dfmi_qmm_prepare": (_int, [_int, ctypes.POINTER(QmmSegment), _int, _c_void_p, _i64, _i64,
+                                _i64, _int, _int, _c_void_p, _size, _c_void_p, _size]),
+    "dfmi_qmm_run": (_int, [_c_void_p] * 7),
     "dfmi_gather_qmm_affine": (_int, [_c_void_p, _int, _i64, _c_void_p, _c_void_p, _c_void_p,
                                       _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64,
                                       _int, _int, _c_void_p]),

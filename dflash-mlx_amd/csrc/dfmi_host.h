@@ -42,12 +42,3 @@ inline bool stream_eligible(int64_t M, int64_t K, int64_t N, int gs, int bits = 
 int dfmi_qmm8_launch(const void* x, int x_dtype, const uint32_t* w_q, const void* scales,
                      const void* biases, void* y, int64_t M, int64_t K, int64_t N, int gs,
                      void* stream);
-
-// Persistent streaming kernel (dfmi_persist.hip): plan query (eligible and
-// planned; workspace bytes) and launch, called by the qmm entry points after
-// their argument checks.
-bool dfmi_persist_plan(int64_t M, int64_t K, const int64_t* Ns, int nseg, int gs, int bits,
-                       size_t* ws_bytes);
-int dfmi_persist_launch(const void* x, int x_dtype, const dfmi_qmm_segment* segs, int nseg,
-                        int64_t M, int64_t K, int gs, void* workspace, size_t workspace_bytes,
-                        void* stream);

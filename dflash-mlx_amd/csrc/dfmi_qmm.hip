@@ -141,12 +141,6 @@ static void launch_tag(int gs, const DensePlan& p, hipStream_t st, const DenseAr
 // no plain store is published across workgroups.
 
 constexpr size_t kCounterBytes = 65536;
-// The persistent wide kernel (dfmi_persist.hip) as the automatic choice for
-// plain and shared-activation calls: off.  On MI355X it measured slower than
-// the streaming grid on every M = 16 verify shape (27B q/k/v fused 18.8 vs
-// 12.0 us, gate/up fused 40.9 vs 33.4 us, 151936 x 5120 137 vs 106 us), so it
-// runs only when tuning path 3 asks for it.
-constexpr bool kPersistAuto = false;
 constexpr int kMaxCounters = (int)(kCounterBytes / 4);
 constexpr int kMaxSeg = 4;  // weight matrices of one shared-activation launch
 
@@ -182,6 +176,10 @@ struct StreamSegs {
   // [K/GS][sum of N] pair table of all the matrices side by side (each
   // segment's own t then unused), or null: qmm_stream_fused_kernel
   const uint32_t* fused;
+  // the row length (in pairs) of the table every segment's t points into
+  // (each t its matrix's column slice of a wider table: column 0 of the
+  // slice), or 0 when each t is its matrix's own [K/GS][N] table
+  uint32_t tn;
 };
 
 // workgroup L -> (block nb, K split kpi of kpw).  Workgroups [0, whole) take
@@ -588,14 +586,15 @@ static int plan_stream(int64_t M, int64_t K, int64_t N, int gs, int bits,
 // preloaded into SGPRs at wave start (-amdgpu-kernarg-preload-count): the
 // hardware preloads 14 dwords on gfx950, so everything the first DMA needs
 // comes first (x, w, t, s, b, a packed word M | xcd_map << 6 | kp << 7 |
-// chunks << 16, N, whole; the block count and K follow from N and chunks)
-// and the outputs and split-K workspace, first needed in the epilogue, last.
-// (With M, K, N ... after the eight pointers a workgroup waited for one
-// scalar-load round trip before its first DMA.)
+// chunks << 16, N, whole, the pair table's row length tn (0: N); the block
+// count and K follow from N and chunks) and the outputs and split-K
+// workspace, first needed in the epilogue, last.  (With M, K, N ... after
+// the eight pointers a workgroup waited for one scalar-load round trip
+// before its first DMA.)
 template <typename Tag, int GS, int MT, int WV, int BITS, int SBPC, bool TSB, int RW>
 __global__ __launch_bounds__(64 * WV) void qmm_stream_kernel(
     const uint16_t* x, const uint32_t* w, const uint32_t* t, const uint16_t* s,
-    const uint16_t* b, uint32_t p0, int N, int whole, uint16_t* y, float* partials,
+    const uint16_t* b, uint32_t p0, int N, int whole, uint32_t tn, uint16_t* y, float* partials,
     uint32_t* counters) {
   using S = Stream<Tag, GS, MT, WV, SBPC, BITS, RW, TSB>;
   const int M = (int)(p0 & 63u), xcd_map = (int)((p0 >> 6) & 1u), kp = (int)((p0 >> 7) & 511u);
@@ -607,7 +606,7 @@ __global__ __launch_bounds__(64 * WV) void qmm_stream_kernel(
   qmm_stream_body<Tag, GS, MT, WV, BITS, SBPC, TSB, RW>(
       StreamArgs{x, partials, counters, M, chunks * S::CK, chunks, kp, n_blocks, xcd_map,
                  kStreamRows * RW * (n_blocks - whole), whole},
-      StreamSeg{w, s, b, y, N, 0, t}, nb, kpi, kpw);
+      StreamSeg{w, s, b, y, N, 0, t}, nb, kpi, kpw, tn, 0u);
 }
 
 // Several weight matrices over the same activations (q / k / v, gate / up):
@@ -622,7 +621,7 @@ __global__ __launch_bounds__(64 * WV) void qmm_stream_multi_kernel(StreamArgs a,
 #pragma unroll
   for (int i = 1; i < kMaxSeg; ++i)
     if (i < m.nseg && nb >= m.seg[i].blk0) g = m.seg[i];
-  qmm_stream_body<Tag, GS, MT, WV, BITS, SBPC, TSB, RW>(a, g, nb, kpi, kpw);
+  qmm_stream_body<Tag, GS, MT, WV, BITS, SBPC, TSB, RW>(a, g, nb, kpi, kpw, m.tn, 0u);
 }
 
 // Two or three matrices over the same activations whose pair tables sit side
@@ -667,10 +666,12 @@ __global__ __launch_bounds__(64 * WV) void qmm_stream_fused_kernel(
 
 // The fused kernel takes the launch: two or three matrices, each N < 2^16,
 // and the plan's values fit their packed fields.
+// (Every matrix's N a multiple of 4 as well: each lane's 16-byte load of
+// pairs then starts on a 16-byte boundary of the combined table.)
 static bool fused_fits(const StreamSegs& m, int whole, int kp, int chunks, int M) {
   if (!m.fused || m.nseg < 2 || m.nseg > 3) return false;
   for (int i = 0; i < m.nseg; ++i)
-    if (m.seg[i].N >= 65536) return false;
+    if (m.seg[i].N >= 65536 || m.seg[i].N % 4) return false;
   return whole < 65536 && kp < 128 && chunks < 65536 && M < 64;
 }
 
@@ -694,8 +695,8 @@ static void launch_stream_k(const StreamPlan& p, hipStream_t st, const StreamArg
     const uint32_t p0 = (uint32_t)a.M | ((uint32_t)a.xcd_map << 6) | ((uint32_t)a.kp << 7) |
                         ((uint32_t)a.chunks << 16);
     hipLaunchKernelGGL((qmm_stream_kernel<Tag, GS, MT, WV, BITS, SBPC, TSB, RW>), dim3(p.grid_x),
-                       dim3(64 * WV), lds, st, a.x, g.w, g.t, g.s, g.b, p0, g.N, a.whole, g.y,
-                       a.partials, a.counters);
+                       dim3(64 * WV), lds, st, a.x, g.w, g.t, g.s, g.b, p0, g.N, a.whole, m.tn,
+                       g.y, a.partials, a.counters);
   } else {
     if constexpr (TSB && BITS == 4 && GS >= 64) {
       if (m.fused) {  // fused_fits() held when the plan was made
@@ -860,32 +861,27 @@ static bool use_stream(int64_t M, int64_t K, int64_t N, int gs, int bits,
          ((N + kStreamRows - 1) / kStreamRows <= kMaxCounters || K / gs <= sb_max_groups(sbpc));
 }
 
-// tuning.path: 0 automatic, 1 general kernel, 2 streaming kernel, 3 persistent
-// streaming kernel
+// tuning.path: 0 automatic, 1 general kernel, 2 streaming kernel
 static bool valid_path(const dfmi_qmm_tuning* tune) {
-  return !tune || (tune->path >= 0 && tune->path <= 3);
+  return !tune || (tune->path >= 0 && tune->path <= 2);
 }
 
-// The persistent streaming kernel takes a plain call when path 3 (or the
-// automatic choice, with kPersistAuto) asks for it and its planner accepts the
-// shape.
-static bool use_persist(int64_t M, int64_t K, int64_t N, int gs, int bits,
-                        const dfmi_qmm_tuning* tune, size_t* ws) {
-  const int path = tune ? tune->path : 0;
-  if (path != 0 && path != 3) return false;
-  if (path == 0 && tune && (tune->k_splits || tune->waves_per_block || tune->tiles_per_wave))
-    return false;  // explicit split / wave choices address the per-call grid
-  if (path == 0 && !kPersistAuto) return false;
-  return dfmi_persist_plan(M, K, &N, 1, gs, bits, ws);
-}
-
-// The streaming kernel over the matrices of m (their row blocks one grid of
-// n_cols / 64 blocks), after the caller's argument checks.
-static int launch_streaming(const void* x, int x_dtype, const StreamSegs& segs, int64_t M,
-                            int64_t K, int64_t n_cols, int gs, int bits,
-                            const dfmi_qmm_tuning* tuning, void* workspace,
-                            size_t workspace_bytes, hipStream_t st) {
+// Everything a streaming launch needs except the activations, the outputs
+// and the stream: the plan, the kernel arguments and the matrices.
+struct StreamLaunch {
   StreamPlan p;
+  StreamArgs a;
+  StreamSegs m;
+  int x_dtype;
+  int gs;
+};
+
+// Plan the streaming kernel over the matrices of segs (their row blocks one
+// grid of n_cols / 64 blocks), after the caller's argument checks.
+static int prepare_streaming(int x_dtype, const StreamSegs& segs, int64_t M, int64_t K,
+                             int64_t n_cols, int gs, int bits, const dfmi_qmm_tuning* tuning,
+                             void* workspace, size_t workspace_bytes, StreamLaunch& L) {
+  StreamPlan& p = L.p;
   int64_t Ns[kMaxSeg];
   for (int i = 0; i < segs.nseg; ++i) Ns[i] = segs.seg[i].N;
   const int rc = plan_stream(M, K, n_cols, gs, bits, tuning, p, Ns, segs.nseg);
@@ -901,14 +897,15 @@ static int launch_streaming(const void* x, int x_dtype, const StreamSegs& segs, 
   if (sg.fused && !(p.tsb && fused_fits(sg, p.whole, p.kp, p.chunks, (int)M))) sg.fused = nullptr;
   if (p.rw == 2 && !segs_have_pairs(sg)) plan_as_rows64(p);
   // each matrix's first block in the launch's block size
-  StreamSegs m = sg;
+  StreamSegs& m = L.m;
+  m = sg;
   int blk = 0;
   for (int i = 0; i < m.nseg; ++i) {
     m.seg[i].blk0 = blk;
     blk += (int)((Ns[i] + kStreamRows * p.rw - 1) / (kStreamRows * p.rw));
   }
-  StreamArgs a;
-  a.x = static_cast<const uint16_t*>(x);
+  StreamArgs& a = L.a;
+  a.x = nullptr;
   a.partials = nullptr;
   a.counters = nullptr;
   if (p.kp > 1) {
@@ -928,10 +925,32 @@ static int launch_streaming(const void* x, int x_dtype, const StreamSegs& segs, 
   a.xcd_map = p.xcd_map;
   a.pstride = kStreamRows * p.rw * (p.n_blocks - p.whole);
   a.whole = p.whole;
+  L.x_dtype = x_dtype;
+  L.gs = gs;
   allow_lds_all();
-  if (x_dtype == DFMI_BF16) launch_stream<BF16>(gs, p, st, a, m);
-  else launch_stream<F16>(gs, p, st, a, m);
-  return check_launch(m.nseg == 1 ? "dfmi_qmm_affine" : "dfmi_qmm_affine_multi");
+  return DFMI_OK;
+}
+
+// Launch a prepared streaming plan on x (the outputs are in L.m).
+static int run_streaming(const StreamLaunch& L, const void* x, hipStream_t st) {
+  StreamArgs a = L.a;
+  a.x = static_cast<const uint16_t*>(x);
+  if (L.x_dtype == DFMI_BF16) launch_stream<BF16>(L.gs, L.p, st, a, L.m);
+  else launch_stream<F16>(L.gs, L.p, st, a, L.m);
+  return check_launch(L.m.nseg == 1 ? "dfmi_qmm_affine" : "dfmi_qmm_affine_multi");
+}
+
+// The streaming kernel over the matrices of segs, after the caller's
+// argument checks.
+static int launch_streaming(const void* x, int x_dtype, const StreamSegs& segs, int64_t M,
+                            int64_t K, int64_t n_cols, int gs, int bits,
+                            const dfmi_qmm_tuning* tuning, void* workspace,
+                            size_t workspace_bytes, hipStream_t st) {
+  StreamLaunch L;
+  const int rc = prepare_streaming(x_dtype, segs, M, K, n_cols, gs, bits, tuning, workspace,
+                                   workspace_bytes, L);
+  if (rc != DFMI_OK) return rc;
+  return run_streaming(L, x, st);
 }
 
 // Shared-activation launches take the streaming kernel when every matrix
@@ -954,8 +973,6 @@ extern "C" size_t dfmi_qmm_workspace_bytes_ex(int64_t M, int64_t K, int64_t N, i
   if (validate_qmm(DFMI_BF16, M, K, N, group_size, bits) != DFMI_OK || M == 0 || N == 0 ||
       !valid_path(tuning))
     return 0;
-  size_t pws = 0;
-  if (use_persist(M, K, N, group_size, bits, tuning, &pws)) return pws;
   if (!use_stream(M, K, N, group_size, bits, tuning)) return 0;
   StreamPlan p;
   if (plan_stream(M, K, N, group_size, bits, tuning, p) != DFMI_OK) return 0;
@@ -976,8 +993,7 @@ extern "C" int dfmi_qmm_plan(int64_t M, int64_t K, const int64_t* Ns, int nseg, 
   *out = dfmi_qmm_plan_info{};
   int64_t cols = 0;
   if (nseg == 1) {
-    if (use_persist(M, K, Ns[0], group_size, bits, tuning, nullptr) ||
-        !use_stream(M, K, Ns[0], group_size, bits, tuning))
+    if (!use_stream(M, K, Ns[0], group_size, bits, tuning))
       return DFMI_OK;  // not the streaming kernel: streaming = 0
     cols = Ns[0];
   } else {
@@ -1002,8 +1018,6 @@ extern "C" const char* dfmi_qmm_kernel_name(int64_t M, int64_t K, int64_t N, int
                                              int bits, const dfmi_qmm_tuning* tuning) {
   if (validate_qmm(DFMI_BF16, M, K, N, group_size, bits) != DFMI_OK || !valid_path(tuning))
     return nullptr;
-  if (use_persist(M, K, N, group_size, bits, tuning, nullptr)) return "qmm_persist_kernel";
-  if (tuning && tuning->path == 3) return nullptr;
   if (bits == 8) return use_stream(M, K, N, group_size, bits, tuning) ? "qmm8_stream_kernel"
                                                                       : "qmm8_kernel";
   return use_stream(M, K, N, group_size, bits, tuning) ? "qmm_stream_kernel" : "qmm_dense_kernel";
@@ -1035,13 +1049,6 @@ extern "C" int dfmi_qmm_affine_pairs(const void* x, int x_dtype, const uint32_t*
               (long long)M, (long long)K, (long long)N, group_size, bits);
     return DFMI_EINVAL;
   }
-  size_t pws = 0;
-  const bool persist = use_persist(M, K, N, group_size, bits, tuning, &pws);
-  if (tuning && tuning->path == 3 && !persist) {
-    set_error("dfmi_qmm: shape M=%lld K=%lld N=%lld gs=%d bits=%d outside the persistent kernel",
-              (long long)M, (long long)K, (long long)N, group_size, bits);
-    return DFMI_EINVAL;
-  }
   if (!x || !w_q || !scales || !biases || !y) {
     set_error("dfmi_qmm: null pointer");
     return DFMI_EINVAL;
@@ -1050,11 +1057,6 @@ extern "C" int dfmi_qmm_affine_pairs(const void* x, int x_dtype, const uint32_t*
       (sb_pairs && !aligned16(sb_pairs))) {
     set_error("dfmi_qmm: x, w_q, scales, biases and sb_pairs must be 16-byte aligned");
     return DFMI_EINVAL;
-  }
-  if (persist) {
-    const dfmi_qmm_segment seg{w_q, scales, biases, y, N};
-    return dfmi_persist_launch(x, x_dtype, &seg, 1, M, K, group_size, workspace,
-                               workspace_bytes, stream);
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
   // 8-bit: the streaming kernel where it applies, else the register-load kernel
@@ -1123,12 +1125,16 @@ __global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* p, int n) {
   for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) p[i] = 0u;
 }
 
-// This device's copy of `scratch`; on its first call per device the counter
-// region is cleared by a kernel on `st` (ahead of the caller's launch in
-// stream order; a kernel node, so graph capture may record it).
+// This device's copy of `scratch`.  Until a call on the device has run
+// outside graph capture, each call first clears the counter region with a
+// kernel on `st` (ahead of the caller's launch in stream order).  A call
+// under capture records that clear into the graph, so every replay starts
+// from zero counters, and does not count as the device's first call: the
+// graph may never be replayed, so the next uncaptured call clears again.
 static int scratch_of_device(hipStream_t st, void** out) {
   static std::mutex mu;
   static void* ptrs[kScratchDevices] = {};
+  static bool cleared[kScratchDevices] = {};
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess || dev < 0 || dev >= kScratchDevices) {
@@ -1145,11 +1151,20 @@ static int scratch_of_device(hipStream_t st, void** out) {
                 dev, hipGetErrorString(e));
       return DFMI_ELAUNCH;
     }
-    hipLaunchKernelGGL(zero_words_kernel, dim3(64), dim3(256), 0, st, static_cast<uint32_t*>(p),
-                       (int)(kCounterBytes / 4));
+    ptrs[dev] = p;
+  }
+  if (!cleared[dev]) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing(st, &cap);
+    if (e != hipSuccess) {
+      set_error("dfmi_qmm_affine_noalloc: hipStreamIsCapturing failed: %s", hipGetErrorString(e));
+      return DFMI_ELAUNCH;
+    }
+    hipLaunchKernelGGL(zero_words_kernel, dim3(64), dim3(256), 0, st,
+                       static_cast<uint32_t*>(ptrs[dev]), (int)(kCounterBytes / 4));
     const int rc = check_launch("dfmi_qmm_affine_noalloc (scratch clear)");
     if (rc != DFMI_OK) return rc;
-    ptrs[dev] = p;
+    if (cap == hipStreamCaptureStatusNone) cleared[dev] = true;
   }
   *out = ptrs[dev];
   return DFMI_OK;
@@ -1186,8 +1201,6 @@ extern "C" size_t dfmi_qmm_multi_workspace_bytes(int64_t M, int64_t K, const int
   for (int i = 0; i < nseg; ++i)
     if (validate_qmm(DFMI_BF16, M, K, Ns[i], group_size, bits) != DFMI_OK) return 0;
   if (M == 0) return 0;
-  size_t pws = 0;
-  if (kPersistAuto && dfmi_persist_plan(M, K, Ns, nseg, group_size, bits, &pws)) return pws;
   const int64_t cols = multi_stream_cols(M, K, Ns, nseg, group_size, bits);
   if (cols > 0) {
     StreamPlan p;
@@ -1205,8 +1218,6 @@ extern "C" const char* dfmi_qmm_multi_kernel_name(int64_t M, int64_t K, const in
   if (!Ns || nseg < 1 || nseg > kMaxSeg) return nullptr;
   for (int i = 0; i < nseg; ++i)
     if (validate_qmm(DFMI_BF16, M, K, Ns[i], group_size, bits) != DFMI_OK) return nullptr;
-  if (kPersistAuto && dfmi_persist_plan(M, K, Ns, nseg, group_size, bits, nullptr))
-    return "qmm_persist_kernel";
   if (multi_stream_cols(M, K, Ns, nseg, group_size, bits) <= 0) return nullptr;
   return nseg == 1 ? "qmm_stream_kernel" : "qmm_stream_multi_kernel";
 }
@@ -1244,9 +1255,6 @@ static int qmm_multi(const void* x, int x_dtype, const dfmi_qmm_segment* segs, i
       return DFMI_EINVAL;
     }
   }
-  if (kPersistAuto && dfmi_persist_plan(M, K, Ns, nseg, group_size, bits, nullptr))
-    return dfmi_persist_launch(x, x_dtype, segs, nseg, M, K, group_size, workspace,
-                               workspace_bytes, stream);
   const int64_t cols = multi_stream_cols(M, K, Ns, nseg, group_size, bits);
   if (cols > 0) {
     StreamSegs m{};
@@ -1291,6 +1299,159 @@ extern "C" int dfmi_qmm_affine_multi_fused(const void* x, int x_dtype,
   }
   return qmm_multi(x, x_dtype, segs, nseg, sb_pairs, M, K, group_size, bits, workspace,
                    workspace_bytes, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Prepared launches (dfmi_qmm_prepare / dfmi_qmm_run): the plan, the kernel
+// arguments and the matrices of a verify linear (or of sibling projections
+// sharing their input) computed once, so that each call is one short C call.
+
+namespace dfmi {
+
+constexpr uint64_t kRecordMagic = 0x6466'6d69'7265'6301ull;  // "dfmirec", version 1
+
+struct QmmRecord {
+  uint64_t magic;
+  int kind;  // 1: streaming launch (L); 2: dfmi_qmm_affine_multi_fused call with the stored arguments
+  int nseg;
+  StreamLaunch L;
+  // kind 2
+  dfmi_qmm_segment segs[kMaxSeg];
+  const uint32_t* fused;
+  int x_dtype, gs, bits;
+  int64_t M, K;
+  void* workspace;
+  size_t workspace_bytes;
+};
+static_assert(sizeof(QmmRecord) <= DFMI_QMM_RECORD_BYTES, "record buffer");
+static_assert(alignof(QmmRecord) <= 16, "record alignment");
+
+}  // namespace dfmi
+
+extern "C" int dfmi_qmm_prepare(int x_dtype, const dfmi_qmm_segment* segs, int nseg,
+                                const uint32_t* fused_pairs, int64_t sb_stride, int64_t M,
+                                int64_t K, int group_size, int bits, void* workspace,
+                                size_t workspace_bytes, void* record, size_t record_bytes) {
+  if (!record || record_bytes < sizeof(QmmRecord) ||
+      (reinterpret_cast<uintptr_t>(record) & 15u)) {
+    set_error("dfmi_qmm_prepare: record buffer of %zu bytes (16-byte aligned) required",
+              sizeof(QmmRecord));
+    return DFMI_EINVAL;
+  }
+  QmmRecord* r = static_cast<QmmRecord*>(record);
+  r->magic = 0;  // invalid until prepared
+  if (!segs || nseg < 1 || nseg > kMaxSeg) {
+    set_error("dfmi_qmm_prepare: 1..%d segments required (got %d)", kMaxSeg, nseg);
+    return DFMI_EINVAL;
+  }
+  int64_t Ns[kMaxSeg];
+  for (int i = 0; i < nseg; ++i) {
+    const int rc = validate_qmm(x_dtype, M, K, segs[i].N, group_size, bits);
+    if (rc != DFMI_OK) return rc;
+    Ns[i] = segs[i].N;
+    if (segs[i].N == 0) continue;
+    if (!segs[i].w_q || !segs[i].scales || !segs[i].biases) {
+      set_error("dfmi_qmm_prepare: null pointer in segment %d", i);
+      return DFMI_EINVAL;
+    }
+    if (!aligned16(segs[i].w_q) || !aligned16(segs[i].scales) || !aligned16(segs[i].biases) ||
+        (segs[i].sb_pairs && !aligned16(segs[i].sb_pairs))) {
+      set_error("dfmi_qmm_prepare: segment %d: w_q, scales, biases and sb_pairs must be 16-byte "
+                "aligned", i);
+      return DFMI_EINVAL;
+    }
+  }
+  if (fused_pairs && !aligned16(fused_pairs)) {
+    set_error("dfmi_qmm_prepare: fused_pairs must be 16-byte aligned");
+    return DFMI_EINVAL;
+  }
+  if (sb_stride != 0) {
+    bool ok = !fused_pairs && sb_stride % 4 == 0 && sb_stride < (1ll << 31) &&
+              sb_stride * (K / group_size) * 4 <= 0xFFFFFFFFll;
+    // (N % 4 == 0: a lane's 16-byte load of four pairs then ends inside its
+    // slice, so nothing past the wider table is read)
+    for (int i = 0; i < nseg; ++i)
+      ok = ok && (Ns[i] == 0 || (segs[i].sb_pairs && Ns[i] <= sb_stride && Ns[i] % 4 == 0));
+    if (!ok) {
+      set_error("dfmi_qmm_prepare: sb_stride %lld needs every matrix's pair table, "
+                "N <= sb_stride, N %% 4 == 0, sb_stride %% 4 == 0 and no fused_pairs",
+                (long long)sb_stride);
+      return DFMI_EINVAL;
+    }
+  }
+  const int64_t cols = nseg == 1 ? (use_stream(M, K, Ns[0], group_size, bits, nullptr) ? Ns[0] : 0)
+                                 : multi_stream_cols(M, K, Ns, nseg, group_size, bits);
+  if (M > 0 && cols > 0) {
+    StreamSegs m{};
+    int blk = 0;
+    for (int i = 0; i < nseg; ++i) {
+      m.seg[i] = StreamSeg{segs[i].w_q, static_cast<const uint16_t*>(segs[i].scales),
+                           static_cast<const uint16_t*>(segs[i].biases), nullptr, (int)Ns[i], blk,
+                           segs[i].sb_pairs};
+      blk += (int)((Ns[i] + kStreamRows - 1) / kStreamRows);
+    }
+    m.nseg = nseg;
+    m.fused = nseg > 1 ? fused_pairs : nullptr;
+    m.tn = (uint32_t)sb_stride;
+    const int rc = prepare_streaming(x_dtype, m, M, K, cols, group_size, bits, nullptr,
+                                     workspace, workspace_bytes, r->L);
+    if (rc != DFMI_OK) return rc;
+    r->kind = 1;
+  } else {
+    // outside the streaming kernel: the shared-activation entry point's own
+    // route at each call (a pair table in a wider one is not passed: the
+    // plans it would serve are all streaming)
+    for (int i = 0; i < nseg; ++i) {
+      r->segs[i] = segs[i];
+      r->segs[i].y = nullptr;
+      if (sb_stride != 0) r->segs[i].sb_pairs = nullptr;
+    }
+    r->fused = fused_pairs;
+    r->kind = 2;
+  }
+  r->nseg = nseg;
+  r->x_dtype = x_dtype;
+  r->gs = group_size;
+  r->bits = bits;
+  r->M = M;
+  r->K = K;
+  r->workspace = workspace;
+  r->workspace_bytes = workspace_bytes;
+  r->magic = kRecordMagic;
+  return DFMI_OK;
+}
+
+extern "C" int dfmi_qmm_run(const void* record, const void* x, void* y0, void* y1, void* y2,
+                            void* y3, void* stream) {
+  const QmmRecord* r = static_cast<const QmmRecord*>(record);
+  if (!r || r->magic != kRecordMagic) {
+    set_error("dfmi_qmm_run: not a prepared record");
+    return DFMI_EINVAL;
+  }
+  if (r->M == 0) return DFMI_OK;
+  if (!x || !aligned16(x)) {
+    set_error("dfmi_qmm_run: x must be a 16-byte aligned device pointer");
+    return DFMI_EINVAL;
+  }
+  void* const ys[kMaxSeg] = {y0, y1, y2, y3};
+  if (r->kind == 1) {
+    StreamLaunch L = r->L;
+    for (int i = 0; i < r->nseg; ++i) {
+      if (L.m.seg[i].N > 0 && !ys[i]) {
+        set_error("dfmi_qmm_run: null output %d", i);
+        return DFMI_EINVAL;
+      }
+      L.m.seg[i].y = static_cast<uint16_t*>(ys[i]);
+    }
+    return run_streaming(L, x, static_cast<hipStream_t>(stream));
+  }
+  dfmi_qmm_segment segs[kMaxSeg];
+  for (int i = 0; i < r->nseg; ++i) {
+    segs[i] = r->segs[i];
+    segs[i].y = ys[i];
+  }
+  return qmm_multi(x, r->x_dtype, segs, r->nseg, r->fused, r->M, r->K, r->gs, r->bits,
+                   r->workspace, r->workspace_bytes, stream);
 }
 
 // ---------------------------------------------------------------------------

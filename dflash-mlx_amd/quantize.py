@@ -7,8 +7,9 @@ torch: per group ``scale = max((max - min) / (2**bits - 1), 1e-7)``, negated
 unless ``|min| > |max|``, ``edge`` = min or max accordingly, the scale is
 snapped to ``edge / round(edge / scale)`` and the bias is ``edge`` (0 when
 that rounds to 0); codes ``clip(round((w - bias) / scale), 0, 2**bits - 1)``
-against the scales / biases as stored in the output dtype.  Packing: word j of
-row n holds ``32/bits`` consecutive k, first k in the lowest bits.
+against the float32 scale and bias, which are then cast to the output dtype
+(MLX's order).  Packing: word j of row n holds ``32/bits`` consecutive k,
+first k in the lowest bits.
 """
 
 from __future__ import annotations
@@ -42,11 +43,9 @@ def quantize(w: torch.Tensor, group_size: int = 64, bits: int = 4,
     nz = q0 != 0
     scale = torch.where(nz, edge / torch.where(nz, q0, torch.ones_like(q0)), scale)
     bias = torch.where(nz, edge, torch.zeros_like(edge))
+    q = torch.round((wf - bias.unsqueeze(-1)) / scale.unsqueeze(-1))
     scales = scale.to(dtype)
     biases = bias.to(dtype)
-    s_r = scales.to(torch.float32).unsqueeze(-1)
-    b_r = biases.to(torch.float32).unsqueeze(-1)
-    q = torch.round((wf - b_r) / s_r)
     q = torch.nan_to_num(q, nan=0.0, posinf=n_bins, neginf=0.0).clamp_(0, n_bins)
     q = q.to(torch.int64).reshape(n, k)
     per = 32 // bits

@@ -25,10 +25,11 @@ from .internal_debug import (
 )
 from .quantize import quantize
 from .verify_qmm import (
+    LaunchRecord,
     _kparts_tuning,
     _m4_ksplit_np_shape,
-    qmm_multi_launch,
     _resolve_m16_ktmpl_variant,
+    current_stream,
     qmm_launch,
     quantized_matmul,
     verify_matmul,
@@ -146,12 +147,81 @@ class VerifyQuantizedLinear(QuantizedLinear):
                        enable_qmm: Optional[bool] = None) -> "VerifyQuantizedLinear":
         obj = cls(ql.weight, ql.scales, ql.biases, getattr(ql, "bias", None),
                   group_size=ql.group_size, bits=ql.bits, mode=getattr(ql, "mode", "affine"))
+        object.__setattr__(obj, "_enable_qmm", enable_qmm)
         object.__setattr__(obj, "_call_fn", _build_dispatch(obj, enable_qmm=enable_qmm))
         obj.requires_grad_(False)
         return obj
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         return self._call_fn(x)
+
+    def _apply(self, fn, recurse=True):
+        # .to() / .cuda() / .half() replace the buffers: the launch state
+        # (packed tensors, pair table, prepared launches) is rebuilt for the
+        # new ones, and the module leaves its sibling group (it then launches
+        # alone; install_verify_linears groups it again)
+        out = super()._apply(fn, recurse)
+        if "_call_fn" in self.__dict__:
+            object.__setattr__(self, "_call_fn",
+                               _build_dispatch(self, enable_qmm=self.__dict__.get("_enable_qmm")))
+        return out
+
+
+_KERNEL_DTYPES = (torch.bfloat16, torch.float16)
+
+
+class _VerifyState:
+    """Launch state of one verify module, built once by ``_build_dispatch``:
+    the packed tensors, the (scale, bias) pair table (the module's own
+    ``[K/gs][N]`` table, or its column slice of its sibling group's combined
+    table, ``stride`` columns per row), the prepared launches per call shape
+    and the sibling group it belongs to."""
+
+    __slots__ = ("w", "s", "b", "N", "K", "gs", "bits", "pairs", "pairs_ok", "stride", "recs",
+                 "group", "gidx")
+
+    def __init__(self, w, s, b, N, K, gs, bits):
+        self.w, self.s, self.b = w, s, b
+        self.N, self.K, self.gs, self.bits = N, K, gs, bits
+        self.pairs = None
+        self.pairs_ok = (s.dtype in _KERNEL_DTYPES and s.device.type == "cuda" and
+                         _runtime.pair_shape(16, K, N, gs, bits))
+        self.stride = 0
+        self.recs = {}
+        self.group = None
+        self.gidx = 0
+
+    def pair_table(self):
+        """The pair table (built on first use; None while a graph is being
+        captured before it exists: the launch then runs without it, with the
+        same plan and bit-identical results)."""
+        if self.pairs is None and self.pairs_ok:
+            if torch.cuda.is_current_stream_capturing():
+                return None
+            self.pairs = _runtime.build_sb_pairs(self.s, self.b)
+        return self.pairs
+
+    def record(self, m: int, st: int, x: torch.Tensor) -> LaunchRecord:
+        """The prepared launch of an [m, K] call on stream st."""
+        key = (m, st, x.dtype)
+        rec = self.recs.get(key)
+        if rec is None:
+            t = self.pair_table() if m <= 32 else None
+            rec = LaunchRecord(m, self.K, x.dtype, x.device, [(self.w, self.s, self.b, t)],
+                               self.gs, self.bits, sb_stride=self.stride if t is not None else 0)
+            if t is not None or not self.pairs_ok or m > 32:
+                self.recs[key] = rec  # (one made without its table is not kept)
+        return rec
+
+    def launch(self, x: torch.Tensor, m: int, st: int) -> torch.Tensor:
+        """This module's own launch on x: [m, N]."""
+        x2 = x.reshape(m, self.K)
+        if not x2.is_contiguous() or x2.data_ptr() & 15:
+            x2 = _runtime.aligned_contiguous(x2)
+        rec = self.recs.get((m, st, x.dtype)) or self.record(m, st, x)
+        y = torch.empty((m, self.N), dtype=x.dtype, device=x.device)
+        rec.run(x2, (y,), st)
+        return y
 
 
 def _build_dispatch(obj: VerifyQuantizedLinear, *, enable_qmm: Optional[bool] = None):
@@ -165,6 +235,8 @@ def _build_dispatch(obj: VerifyQuantizedLinear, *, enable_qmm: Optional[bool] = 
     ktmpl_variant = _resolve_m16_ktmpl_variant(K, N, bits) if qmm_enabled else None
     m16_qmm = qmm_enabled and (ktmpl_variant is not None or (N % 32 == 0 and K % 32 == 0))
     m4_qmm = qmm_enabled and _m4_ksplit_np_shape(K, N, bits)
+    # (M = 16 and M = 4 are the verify routes, every other M the stock one;
+    # on this GPU both are the same kernels and automatic plan)
     # Reference 176-188 picks mma2big_pipe (K_PARTS 8) or mma2big for shapes
     # the K-templated kernels decline; both run the automatic plan here (the
     # K_PARTS values are Metal launch choices), or DFLASH_VERIFY_QMM_KPARTS
@@ -176,40 +248,39 @@ def _build_dispatch(obj: VerifyQuantizedLinear, *, enable_qmm: Optional[bool] = 
                                 group_size=gs, bits=bits, mode=mode)
 
     if m16_qmm or m4_qmm:
-        w_c = _runtime.weight_words(obj.weight)
-        s_c = _runtime.aligned_contiguous(obj.scales)
-        b_c = _runtime.aligned_contiguous(obj.biases)
-        kernel_dtypes = (torch.bfloat16, torch.float16)
-        # the (scale, bias) pair table of the streaming plans, built once per
-        # module on its first GPU call (or by prewarm_verify_kernels), like
-        # the reference's precomputed route; the launch plan and the result
-        # do not depend on it, so a call under graph capture before it exists
-        # runs without it
-        pair_state = [None, obj.scales.dtype in kernel_dtypes and
-                      _runtime.pair_shape(16, K, N, gs, bits)]
-
-        def pairs_of():
-            if pair_state[0] is None and pair_state[1]:
-                if torch.cuda.is_current_stream_capturing():
-                    return None
-                pair_state[0] = _runtime.build_sb_pairs(s_c, b_c)
-            return pair_state[0]
-
-        object.__setattr__(obj, "_packed", (w_c, s_c, b_c))
-        object.__setattr__(obj, "_pairs_of", pairs_of)
+        state = _VerifyState(_runtime.weight_words(obj.weight),
+                             _runtime.aligned_contiguous(obj.scales),
+                             _runtime.aligned_contiguous(obj.biases), N, K, gs, bits)
+        # the pair table is built with the route, as the reference evaluates
+        # the module's tensors at install (verify_linear.py:148-154), so that a
+        # graph captured later finds it
+        if state.pairs_ok and not torch.cuda.is_current_stream_capturing():
+            state.pair_table()
+        object.__setattr__(obj, "_verify_state", state)
+        # the kernels read scales / biases in the activation dtype: other
+        # inputs go to the stock path, which rejects them
+        sdt = state.s.dtype if state.s.dtype in _KERNEL_DTYPES else None
 
         def call(x: torch.Tensor) -> torch.Tensor:
-            orig = x.shape
-            m = math.prod(int(d) for d in orig[:-1])
-            if x.dtype in kernel_dtypes and ((m == 16 and m16_qmm) or (m == 4 and m4_qmm)):
-                sib = obj.__dict__.get("_sibling")
-                if sib is not None:
-                    y = sib[0].product(sib[1], x, m).reshape(*orig[:-1], N)
+            shp = x.shape
+            kx = shp[-1]
+            m = x.numel() // kx if kx else 0
+            if x.dtype == sdt and x.is_cuda and 0 < m <= 32 and kx == K:
+                if m == 16 and m16_tuning is not None:
+                    x2 = _runtime.aligned_contiguous(x.reshape(m, kx))
+                    y = qmm_launch(x2, state.w, state.s, state.b, N, gs, bits, m16_tuning)
                 else:
-                    x2 = _runtime.aligned_contiguous(x.reshape(m, orig[-1]))
-                    tuning = m16_tuning if m == 16 else None
-                    y = qmm_launch(x2, w_c, s_c, b_c, N, gs, bits, tuning,
-                                   pairs=pairs_of()).reshape(*orig[:-1], N)
+                    # M = 16 / M = 4 (the verify routes) and the other small M
+                    # (the stock route) run the same automatic plan, through
+                    # the module's prepared launch or its sibling group's
+                    # shared one; alone, bit-identical to verify_matmul /
+                    # quantized_matmul on these tensors
+                    st = current_stream(x.get_device())
+                    grp = state.group
+                    y = grp.product(state.gidx, x, m, st) if grp is not None else None
+                    if y is None:
+                        y = state.launch(x, m, st)
+                y = y.view(*shp[:-1], N)
             else:
                 y = _stock(x)
             return y + bias if bias is not None else y
@@ -245,16 +316,22 @@ def _set_module(model: nn.Module, path: str, new: nn.Module) -> None:
 
 def prewarm_verify_kernels(model: nn.Module, *, input_dtype: torch.dtype = torch.bfloat16) -> int:
     """dflash_mlx/verify_linear.py:311-336: one M=16 (and M=4 when eligible)
-    call per unique (K, N, bits, group_size); also sizes this stream's
-    workspace so later calls (and graph captures) do not allocate it, and
-    builds every verify module's pair table."""
+    call per unique (K, N, bits, group_size); also builds every verify
+    module's pair table and prepared launches and sizes this stream's
+    workspace, so that later calls (and graph captures) neither allocate nor
+    plan.  Sibling groups are warmed as groups and then reset (the warm-up
+    calls leave no outputs pending)."""
     seen: set[tuple] = set()
+    groups = {}
     warmed = 0
     for _, m in _leaf_modules(model):
         if not isinstance(m, VerifyQuantizedLinear):
             continue
-        if "_pairs_of" in m.__dict__:
-            m._pairs_of()
+        state = m.__dict__.get("_verify_state")
+        if state is not None:
+            state.pair_table()
+            if state.group is not None:
+                groups[id(state.group)] = state.group
         K = int(m.weight.shape[1]) * (32 // m.bits)
         N = int(m.weight.shape[0])
         key = (K, N, m.bits, m.group_size)
@@ -267,6 +344,8 @@ def prewarm_verify_kernels(model: nn.Module, *, input_dtype: torch.dtype = torch
         if _m4_ksplit_np_shape(K, N, m.bits):
             m(torch.zeros((1, 4, K), dtype=input_dtype, device=dev))
             warmed += 1
+    for grp in groups.values():
+        grp.warm(input_dtype)
     return warmed
 
 
@@ -276,57 +355,164 @@ _SIBLING_SETS = (("q_proj", "k_proj", "v_proj"), ("gate_proj", "up_proj"))
 
 
 class SiblingGroup:
-    """Verify modules of one parent that read the same input: the first member
-    called with a verify-sized input computes every member's product in one
-    ``dfmi_qmm_affine_multi`` launch; the others return theirs when they are
-    called with the same tensor (same storage, version, shape, strides and
-    stream) -- in the model's call order, with no change to the model code.
-    A member called with any other input recomputes the group."""
+    """Verify modules of one parent that read the same input (q/k/v, gate/up).
 
-    def __init__(self, members):
-        self.members = list(members)
-        self._key = None
-        self._ys = None
-        self._taken: set[int] = set()
+    The first member called with an input of at most 32 rows computes the
+    product of every active member in one shared-activation launch
+    (``dfmi_qmm_run`` on the group's prepared launch, the members' pair
+    tables side by side in one combined table); each other member returns
+    its own product when it is called with the same tensor object, unchanged
+    (same ``_version``) and on the same stream -- in the model's call order,
+    with no change to the model code.  The group holds that input until every
+    active member has taken its output, so its storage cannot be reused for
+    another tensor meanwhile.  A member called with any other input launches
+    the group again.
 
-    def product(self, idx: int, x: torch.Tensor, m: int) -> torch.Tensor:
-        key = (x.data_ptr(), x._version, tuple(x.shape), tuple(x.stride()), x.dtype,
-               _runtime.stream_ptr(x.device))
-        if self._ys is not None and self._key == key and idx not in self._taken:
-            y = self._ys[idx]
-        else:
-            x2 = _runtime.aligned_contiguous(x.reshape(m, int(x.shape[-1])))
-            first = self.members[0]
-            self._ys = qmm_multi_launch(x2, [(*mem._packed, mem._pairs_of())
-                                             for mem in self.members],
-                                        first.group_size, first.bits)
-            self._key = key
-            self._taken = set()
-            y = self._ys[idx]
-        self._taken.add(idx)
-        if len(self._taken) == len(self.members):
-            self._key, self._ys, self._taken = None, None, set()  # drop the references
+    A member that leaves its output untaken in two launches running (a layer
+    that never calls it, e.g. a shared-KV attention calling q_proj only, or
+    ``v_proj`` when k == v) drops out of the shared launch and runs its own
+    launch when called; with fewer than two active members left the group
+    launches nothing.  Every member's result equals ``quantized_matmul_multi``
+    over the active members (plus its bias) bit for bit, and is within fp32
+    summation order of the member's own launch."""
+
+    def __init__(self, states, fused: Optional[torch.Tensor], stride: int):
+        self.states = list(states)
+        self.active = tuple(range(len(self.states)))
+        self.fused = fused
+        self.stride = stride
+        self._miss = [0] * len(self.states)
+        self._recs: dict = {}
+        self._x = None
+        self._ver = -1
+        self._st = 0
+        self._ys: dict = {}
+
+    def reset(self) -> None:
+        """Forget any pending outputs (and the held input) and the miss
+        counts, and take every member back into the shared launch."""
+        self._x, self._ver, self._st, self._ys = None, -1, 0, {}
+        self._miss = [0] * len(self.states)
+        self.active = tuple(range(len(self.states)))
+
+    def _record(self, m: int, st: int, x: torch.Tensor) -> LaunchRecord:
+        key = (m, st, x.dtype, self.active)
+        rec = self._recs.get(key)
+        if rec is None:
+            sts = [self.states[j] for j in self.active]
+            first = sts[0]
+            tabs = [st_.pair_table() for st_ in sts]
+            # the combined table serves the launch of every member (the
+            # fused kernel: two or three matrices of fewer than 2^16 rows);
+            # otherwise each matrix reads its column slice of it
+            if (self.fused is not None and len(self.active) == len(self.states)
+                    and 2 <= len(sts) <= 3 and all(q.N < 65536 for q in sts)):
+                rec = LaunchRecord(m, first.K, x.dtype, x.device,
+                                   [(q.w, q.s, q.b) for q in sts], first.gs, first.bits,
+                                   fused=self.fused)
+            elif all(t is not None for t in tabs):
+                rec = LaunchRecord(m, first.K, x.dtype, x.device,
+                                   [(q.w, q.s, q.b, t) for q, t in zip(sts, tabs)], first.gs,
+                                   first.bits, sb_stride=self.stride)
+            else:
+                rec = LaunchRecord(m, first.K, x.dtype, x.device,
+                                   [(q.w, q.s, q.b) for q in sts], first.gs, first.bits)
+            self._recs[key] = rec
+        return rec
+
+    def warm(self, dtype: torch.dtype) -> None:
+        """Reset (the members' own warm-up calls leave outputs untaken), then
+        prepare and run once the shared launch at M=16 and M=4 on the current
+        stream, and reset again."""
+        self.reset()
+        if len(self.active) >= 2:
+            first = self.states[self.active[0]]
+            dev = first.w.device
+            st = current_stream(dev.index if dev.index is not None else
+                                torch.cuda.current_device())
+            for m in (16, 4):
+                x = torch.zeros((m, first.K), dtype=dtype, device=dev)
+                rec = self._record(m, st, x)
+                rec.run(x, [torch.empty((m, self.states[j].N), dtype=dtype, device=dev)
+                             for j in self.active], st)
+        self.reset()
+
+    def product(self, idx: int, x: torch.Tensor, m: int, st: int) -> Optional[torch.Tensor]:
+        """Member idx's [m, N] product of x, or None when idx is not in the
+        shared launch (the member then launches alone)."""
+        ys = self._ys
+        if ys and self._x is x and self._ver == x._version and self._st == st:
+            y = ys.pop(idx, None)
+            if y is not None:
+                self._miss[idx] = 0
+                if not ys:
+                    self._x = None  # every output taken: let the input go
+                return y
+        if idx not in self.active:
+            return None
+        if ys:  # members that did not take the previous launch's output
+            keep = []
+            for j in self.active:
+                if j in ys:
+                    self._miss[j] += 1
+                if self._miss[j] < 2:
+                    keep.append(j)
+            self.active = tuple(keep) if len(keep) >= 2 else ()
+            self._ys = {}
+            if idx not in self.active:
+                self._x = None
+                return None
+        x2 = x.reshape(m, int(x.shape[-1]))
+        if not x2.is_contiguous() or x2.data_ptr() & 15:
+            x2 = _runtime.aligned_contiguous(x2)
+        rec = self._recs.get((m, st, x.dtype, self.active)) or self._record(m, st, x)
+        outs = [torch.empty((m, self.states[j].N), dtype=x.dtype, device=x.device)
+                for j in self.active]
+        rec.run(x2, outs, st)
+        ys = dict(zip(self.active, outs))
+        y = ys.pop(idx)
+        self._miss[idx] = 0
+        self._ys = ys
+        self._x, self._ver, self._st = (x, x._version, st) if ys else (None, -1, 0)
         return y
 
 
 def _group_siblings(model: nn.Module) -> int:
     """Attach a SiblingGroup to each set of sibling verify modules of one
     parent that share K, bits, group size and scale dtype and take the verify
-    kernels; returns the number of groups."""
+    kernels; returns the number of groups.  Where the members have pair
+    tables, their tables are concatenated into the group's combined table
+    and each member keeps only its column slice of it (one copy of the
+    scale data per group)."""
     groups = 0
     for _, parent in model.named_modules():
         for names in _SIBLING_SETS:
             mods = [getattr(parent, n, None) for n in names]
-            if not all(isinstance(m, VerifyQuantizedLinear) and "_packed" in m.__dict__
+            if not all(isinstance(m, VerifyQuantizedLinear) and "_verify_state" in m.__dict__
                        for m in mods):
                 continue
-            sig = {(int(m.weight.shape[1]) * (32 // m.bits), m.bits, m.group_size, m.scales.dtype)
-                   for m in mods}
+            states = [m._verify_state for m in mods]
+            sig = {(q.K, q.bits, q.gs, q.s.dtype, q.s.device) for q in states}
             if len(sig) != 1:
                 continue
-            grp = SiblingGroup(mods)
-            for i, m in enumerate(mods):
-                object.__setattr__(m, "_sibling", (grp, i))
+            for q in states:  # a member of an earlier group leaves it
+                q.group = None
+            fused, stride = None, 0
+            tabs = [q.pair_table() for q in states]
+            if all(t is not None for t in tabs) and all(q.N % 4 == 0 for q in states):
+                # (a member regrouped contributes its column slice of its old
+                # group's table)
+                fused = torch.cat(tabs, dim=1).contiguous()
+                stride = int(fused.shape[1])
+                c = 0
+                for q in states:  # the members' own tables are released
+                    q.pairs = fused[:, c:c + q.N]
+                    q.stride = stride
+                    q.recs = {}
+                    c += q.N
+            grp = SiblingGroup(states, fused, stride)
+            for i, q in enumerate(states):
+                q.group, q.gidx = grp, i
             groups += 1
     return groups
 
@@ -334,15 +520,16 @@ def _group_siblings(model: nn.Module) -> int:
 def install_verify_linears(model: nn.Module, *,
                            predicate: Optional[Callable[[str, QuantizedLinear], bool]] = None,
                            enable_qmm: Optional[bool] = None,
-                           fuse_siblings: bool = False) -> int:
+                           fuse_siblings: bool = True) -> int:
     """dflash_mlx/verify_linear.py:338-361: swap eligible QuantizedLinear
     leaves for VerifyQuantizedLinear; returns the number swapped.
 
-    ``fuse_siblings`` (no reference counterpart, opt-in): group q/k/v and
-    gate/up siblings so each set runs as one shared-activation launch
+    ``fuse_siblings`` (no reference counterpart; on by default): group q/k/v
+    and gate/up siblings so each set runs as one shared-activation launch
     (:class:`SiblingGroup`); every member's output equals what
     ``quantized_matmul_multi`` returns for it (plus its bias), which is
-    within fp32 summation order of the member's own launch."""
+    within fp32 summation order of the member's own launch.  ``False`` keeps
+    one launch per module, each bit-identical to ``verify_matmul``."""
     if predicate is None:
         predicate = lambda path, m: is_verify_eligible(m, path=path)  # noqa: E731
     count = 0

@@ -192,6 +192,79 @@ def qmm_multi_launch(x2: torch.Tensor, mats, group_size: int, bits: int,
     return ys
 
 
+_raw_stream = torch._C._cuda_getCurrentRawStream
+
+
+def current_stream(device_index: int) -> int:
+    """The current HIP stream of a device, as a pointer value."""
+    return int(_raw_stream(device_index))
+
+
+class LaunchRecord:
+    """One prepared launch (``dfmi_qmm_prepare``): the plan, kernel arguments
+    and matrices of a verify linear -- one matrix, or 2..4 sibling matrices
+    sharing their input -- computed once for a call shape (M, dtype, stream),
+    so that a call is one ``dfmi_qmm_run``.  The reference computes each
+    module's route once in ``_build_dispatch`` and launches from a closure
+    (dflash_mlx/verify_linear.py:118-309).
+
+    ``mats``: ``[(w, scales, biases, pairs), ...]`` (``pairs`` None, the
+    matrix's own table, or its column slice of a wider table when
+    ``sb_stride`` names that table's row length); ``fused``: for 2..4
+    matrices, their tables side by side.  The record keeps these tensors and
+    the stream's workspace alive while it exists; run it only on the stream
+    it was prepared for (the workspace is that stream's)."""
+
+    __slots__ = ("_buf", "ptr", "_keep", "M", "Ns", "dtype")
+
+    def __init__(self, M: int, K: int, dtype: torch.dtype, dev: torch.device, mats,
+                 group_size: int, bits: int, fused: Optional[torch.Tensor] = None,
+                 sb_stride: int = 0):
+        lib = _lib.load()
+        n = len(mats)
+        if not 1 <= n <= 4:
+            raise ValueError("1..4 matrices per launch")
+        segs = (_lib.QmmSegment * n)()
+        keep = []
+        Ns = []
+        for i, m in enumerate(mats):
+            w, sc, bi = m[0], m[1], m[2]
+            t = m[3] if len(m) > 3 else None
+            for name, ten in (("w", w), ("scales", sc), ("biases", bi)):
+                if ten.device != dev:
+                    raise ValueError(f"{name} of matrix {i} is on {ten.device}, not {dev}")
+            segs[i].w_q, segs[i].scales, segs[i].biases = w.data_ptr(), sc.data_ptr(), bi.data_ptr()
+            segs[i].N = int(w.shape[0])
+            segs[i].sb_pairs = t.data_ptr() if t is not None else 0
+            keep += [w, sc, bi, t]
+            Ns.append(int(w.shape[0]))
+        if n == 1:
+            need = int(lib.dfmi_qmm_workspace_bytes_ex(M, K, Ns[0], int(group_size), int(bits),
+                                                        None))
+        else:
+            ns = (ctypes.c_int64 * n)(*Ns)
+            need = int(lib.dfmi_qmm_multi_workspace_bytes(M, K, ns, n, int(group_size),
+                                                          int(bits)))
+        ws, ws_bytes = _runtime.workspace(dev, need) if need else (0, 0)
+        buf = ctypes.create_string_buffer(_lib.DFMI_QMM_RECORD_BYTES + 16)
+        ptr = (ctypes.addressof(buf) + 15) // 16 * 16
+        status = lib.dfmi_qmm_prepare(_runtime.dtype_code(dtype), segs, n,
+                                      fused.data_ptr() if fused is not None else 0,
+                                      int(sb_stride), M, K, int(group_size), int(bits), ws,
+                                      ws_bytes, ptr, _lib.DFMI_QMM_RECORD_BYTES)
+        _lib.check(status, "dfmi_qmm_prepare")
+        keep.append(fused)
+        self._buf, self.ptr, self._keep = buf, ptr, keep
+        self.M, self.Ns, self.dtype = M, Ns, dtype
+
+    def run(self, x2: torch.Tensor, ys, stream: int) -> None:
+        """Launch on ``x2 [M, K]`` (contiguous, 16-byte aligned) into ``ys``."""
+        p = [y.data_ptr() for y in ys] + [None] * (4 - len(ys))
+        status = _lib.load().dfmi_qmm_run(self.ptr, x2.data_ptr(), p[0], p[1], p[2], p[3], stream)
+        if status:
+            _lib.check(status, "dfmi_qmm_run")
+
+
 def _prepare(x, w, scales, biases):
     for t, name in ((x, "x"), (w, "w"), (scales, "scales"), (biases, "biases")):
         _runtime.require_device(t, name)

@@ -5,7 +5,9 @@
  * marked "device" is HIP device memory; `stream` is a hipStream_t (NULL = the
  * null stream).  All launches are stream-ordered and asynchronous; a return of
  * DFMI_OK means the work was enqueued.  No function allocates or frees device
- * memory and none keeps a pointer past its return.  Functions are reentrant;
+ * memory and none keeps a pointer past its return (dfmi_qmm_prepare writes
+ * the pointers it is given into the caller's record buffer, which
+ * dfmi_qmm_run then reads).  Functions are reentrant;
  * the process state is the thread-local error string and, for
  * dfmi_qmm_affine_noalloc only, its static device scratch array and the
  * per-device address of it (set once, under a lock).
@@ -52,10 +54,7 @@ const char *dfmi_last_error(void);
  * fields mean "automatic".
  *   path: 1 = general kernel, 2 = streaming kernel (DFMI_EINVAL if the shape
  *         is outside it: M <= 32, K % 256 == 0, K % (8*group_size) == 0;
- *         checked for both weight widths), 3 = persistent stream-K kernel
- *         with 128-row blocks, one workgroup per CU (DFMI_EINVAL outside
- *         M <= 16, int4, K % 256 == 0, K a multiple of 8 groups, at most
- *         16384 blocks); any other value is DFMI_EINVAL;
+ *         checked for both weight widths); any other value is DFMI_EINVAL;
  *   tiles_per_wave: general kernel, 16-row weight tiles per wavefront (1, 2,
  *         4); the streaming kernel always covers 64 rows per workgroup;
  *   waves_per_block: general kernel, wavefronts of a workgroup that split K
@@ -158,7 +157,7 @@ int dfmi_qmm_plan(int64_t M, int64_t K, const int64_t *Ns, int nseg, int group_s
                   const dfmi_qmm_tuning *tuning, dfmi_qmm_plan_info *out);
 /* Host-only plan query (no reference counterpart; for benchmarks and
  * profiles): name of the kernel dfmi_qmm_affine_ex would launch for this
- * shape, "qmm_persist_kernel", "qmm_stream_kernel", "qmm_dense_kernel" or
+ * shape, "qmm_stream_kernel", "qmm_dense_kernel" or
  * (bits 8) "qmm8_stream_kernel" / "qmm8_kernel";
  * NULL if unsupported. */
 const char *dfmi_qmm_kernel_name(int64_t M, int64_t K, int64_t N, int group_size, int bits,
@@ -233,6 +232,39 @@ int dfmi_qmm_affine_multi_fused(const void *x, int x_dtype, const dfmi_qmm_segme
                                 size_t workspace_bytes, void *stream);
 size_t dfmi_qmm_multi_workspace_bytes(int64_t M, int64_t K, const int64_t *Ns, int nseg,
                                       int group_size, int bits);
+
+/*
+ * Prepared launches of a verify linear: the reference's VerifyQuantizedLinear
+ * computes its route once per module in _build_dispatch and its per-call
+ * closure only launches (dflash_mlx/verify_linear.py:118-309, calls at
+ * 266-286); dfmi_qmm_prepare likewise plans one call shape -- one matrix
+ * (dfmi_qmm_affine_pairs) or 2..4 sibling matrices sharing x
+ * (dfmi_qmm_affine_multi / _multi_fused) -- into the caller's record
+ * buffer, and dfmi_qmm_run launches it on new activations and outputs.
+ * Same kernels, plans and results as those entry points (bit-identical).
+ *   segs: the matrices (their y fields are ignored); fused_pairs: for nseg
+ *     >= 2, their pair tables side by side, or NULL;
+ *   sb_stride: the row length (in pairs) of the table that every
+ *     segment's sb_pairs points into when each is its matrix's column slice
+ *     of one wider table (a sibling group's combined table: sb_pairs =
+ *     column 0 of the slice, 16-byte aligned; sb_stride and every N a
+ *     multiple of 4; fused_pairs NULL), else 0;
+ *   workspace: as the matching one-shot entry point needs
+ *     (dfmi_qmm_workspace_bytes_ex / dfmi_qmm_multi_workspace_bytes).
+ * The record (DFMI_QMM_RECORD_BYTES bytes, 16-byte aligned, caller-owned
+ * host memory) keeps the weight, table and workspace pointers: they must
+ * stay valid while the record is used, and calls that run a record (or use
+ * its workspace) concurrently on different streams race.
+ * dfmi_qmm_run: y0..y3 are the outputs of segments 0..nseg-1 ([M, N_i],
+ * x's dtype; unused ones NULL); x 16-byte aligned [M, K].
+ */
+#define DFMI_QMM_RECORD_BYTES 1024
+int dfmi_qmm_prepare(int x_dtype, const dfmi_qmm_segment *segs, int nseg,
+                     const uint32_t *fused_pairs, int64_t sb_stride, int64_t M, int64_t K,
+                     int group_size, int bits, void *workspace, size_t workspace_bytes,
+                     void *record, size_t record_bytes);
+int dfmi_qmm_run(const void *record, const void *x, void *y0, void *y1, void *y2, void *y3,
+                 void *stream);
 /* Host-only plan query (no reference counterpart; for benchmarks and
  * profiles): the kernel of the single launch dfmi_qmm_affine_multi makes,
  * "qmm_stream_multi_kernel" (nseg >= 2) or "qmm_stream_kernel"; NULL when it

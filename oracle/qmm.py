@@ -57,10 +57,10 @@ def quantize(w, group_size: int = 64, bits: int = 4, out_dtype: str = "bf16"):
     snapped to ``edge / q0`` and the bias is ``edge`` (else the bias is 0).
     Codes are ``clip(round((w - bias) / scale), 0, 2**bits - 1)``.
 
-    Arithmetic is float32.  Scales and biases are rounded to ``out_dtype``
-    first and the codes are computed against the rounded values, so that the
-    stored (q, scale, bias) triple reconstructs each group as closely as the
-    stored precision allows.
+    Arithmetic is float32.  The codes are computed against the float32
+    scale and bias; scales and biases are then cast to ``out_dtype`` (MLX's
+    ``affine_quantize`` order: the packing step divides by the unrounded
+    scale, and the returned scales / biases are cast afterwards).
 
     Returns ``(w_q uint32 [N, K*bits/32], scales, biases)`` with scales and
     biases in ``out_dtype`` storage form (uint16 bits for bf16).
@@ -82,15 +82,11 @@ def quantize(w, group_size: int = 64, bits: int = 4, out_dtype: str = "bf16"):
     with np.errstate(divide="ignore", invalid="ignore"):
         scale = np.where(nz, edge / np.where(nz, q0, 1), scale).astype(np.float32)
     bias = np.where(nz, edge, np.float32(0)).astype(np.float32)
-    s_st = round_to_dtype(scale, out_dtype)
-    b_st = round_to_dtype(bias, out_dtype)
-    s_r = to_f32(s_st, out_dtype)[..., None]
-    b_r = to_f32(b_st, out_dtype)[..., None]
     with np.errstate(divide="ignore", invalid="ignore"):
-        qf = np.round((g - b_r) / s_r)
+        qf = np.round((g - bias[..., None]) / scale[..., None])
     qf[np.isnan(qf)] = 0.0
     q = np.clip(qf, 0, n_bins).astype(np.uint8).reshape(n, k)
-    return pack(q, bits), s_st, b_st
+    return pack(q, bits), round_to_dtype(scale, out_dtype), round_to_dtype(bias, out_dtype)
 
 
 def dequantize(w_q, scales, biases, group_size: int, bits: int, dtype: str) -> np.ndarray:

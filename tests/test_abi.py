@@ -77,13 +77,11 @@ def test_host_side_validation_without_gpu(lib):
                                           32, bits, None, 0, ctypes.byref(t), None) \
                 == _lib.DFMI_EINVAL
             assert b"outside the streaming kernel" in lib.dfmi_last_error()
-    # path 3 (the persistent kernel) outside its shapes
+    # path 3 and above are unknown paths
     t3 = _lib.QmmTuning(3, 0, 0, 0)
-    assert lib.dfmi_qmm_affine_ex(None, _lib.DFMI_BF16, None, None, None, None, 24, 4096, 4096,
+    assert lib.dfmi_qmm_affine_ex(None, _lib.DFMI_BF16, None, None, None, None, 16, 4096, 4096,
                                   64, 4, None, 0, ctypes.byref(t3), None) == _lib.DFMI_EINVAL
-    assert b"outside the persistent kernel" in lib.dfmi_last_error()
-    assert lib.dfmi_qmm_kernel_name(16, 4096, 4096, 64, 8, ctypes.byref(t3)) is None
-    assert lib.dfmi_qmm_kernel_name(16, 4096, 4096, 64, 4, ctypes.byref(t3)) == b"qmm_persist_kernel"
+    assert lib.dfmi_qmm_kernel_name(16, 4096, 4096, 64, 4, ctypes.byref(t3)) is None
     # the shared-activation launch: segment count and per-segment checks
     seg = (_lib.QmmSegment * 5)()
     assert lib.dfmi_qmm_affine_multi(None, _lib.DFMI_BF16, seg, 5, 16, 1024, 64, 4, None, 0,

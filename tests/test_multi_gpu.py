@@ -181,3 +181,53 @@ def test_fused_pair_table_bit_identical(dev, M, K, Ns, gs, dtype):
     for g, c in zip(got, cases):  # every matrix multiplies the shared x (cases[0][0])
         if g.size <= (1 << 22):
             _check(g, cases[0][0], c[1], c[2], c[3], gs, dtype)
+
+
+def _gpu_quantized(dev, K, N, dtype, seed):
+    """W ~ N(0, 0.02) [N, K] quantised on the GPU by the product quantiser
+    (bit-identical to the oracle's rule: tests/test_quantize.py)."""
+    import torch
+
+    from dflash_mlx_amd.quantize import quantize
+
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float16
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    w = torch.randn((N, K), generator=gen, device=dev) * 0.02
+    return quantize(w, 64, 4, tdt)
+
+
+@pytest.mark.parametrize("Ns", [(5120, 1024, 1024), (17408, 17408)])
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_fused_launch_27b_m8_m32(dev, Ns, dtype):
+    """The launches the 27B-class M=8 and M=32 sweep lines time: q/k/v
+    (5120 -> 5120/1024/1024) and gate/up (5120 -> 2x17408) through
+    quantized_matmul_multi, i.e. the shared-activation kernel with the
+    matrices' pair tables side by side, against the oracle."""
+    import torch
+
+    from dflash_mlx_amd import _lib, _runtime
+    from dflash_mlx_amd.verify_qmm import quantized_matmul_multi
+
+    K = 5120
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float16
+    mats = [_gpu_quantized(dev, K, N, dtype, seed=300 + i) for i, N in enumerate(Ns)]
+    host = [(w.cpu().numpy().view(np.uint32), from_dev(s, dtype), from_dev(b, dtype))
+            for (w, s, b) in mats]
+    lib = _lib.load()
+    for M in (8, 32):
+        print(f"case: fused 27B launch Ns={Ns} M={M} {dtype}", flush=True)
+        ns = (ctypes.c_int64 * len(Ns))(*Ns)
+        info = _lib.QmmPlanInfo()
+        assert lib.dfmi_qmm_plan(M, K, ns, len(Ns), 64, 4, None, ctypes.byref(info)) == 0
+        assert info.streaming == 1 and info.pair_streaming == 1
+        assert all(_runtime.pair_shape(M, K, N, 64, 4) for N in Ns)
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(400 + M)
+        x = torch.randn((M, K), generator=gen, device=dev).to(tdt)
+        ys = quantized_matmul_multi(x, mats, group_size=64, bits=4)
+        torch.cuda.synchronize()
+        xs = from_dev(x, dtype)
+        for (w_q, s, b), y in zip(host, ys):
+            assert y.shape == (M, w_q.shape[0])
+            _check(from_dev(y, dtype), xs, w_q, s, b, 64, dtype)

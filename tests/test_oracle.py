@@ -64,6 +64,29 @@ def test_quantize_exact_on_affine_grid():
     assert np.all(sc == np.float32(s)) and np.all(bi == np.float32(b))
 
 
+def test_quantize_code_order_known_answer():
+    """MLX's affine_quantize computes the codes against the float32 scale and
+    bias and casts them to the stored dtype afterwards.  A group whose codes
+    differ between that order and codes taken against the stored bf16 scale,
+    worked by hand:
+      w_max = 1.0, w_min = 0.0: |w_min| > |w_max| is false, so
+      scale = -(1 - 0) / 15 = -0.0666667 (float32), edge = w_max = 1.0,
+      q0 = round(1.0 / -0.0666667) = -15 != 0, so scale = 1.0 / -15 and
+      bias = 1.0;
+      w = 0.498667: (w - 1) / scale = 15 * 0.501333 = 7.51999 -> code 8;
+      (against bf16(scale) = -0.06689453125 it would be 7.4943 -> 7);
+      w = 0: 15 -> code 15; w = 1: code 0.
+      Stored scale bf16(-0.0666667) = -0.06689453125 (bits 0xBD89; the
+      neighbours are -0.06640625 and -0.0673828125), bias 1.0 (0x3F80)."""
+    w = np.zeros((1, 64), np.float32)
+    w[0, 0] = 1.0
+    w[0, 1] = np.float32(0.498667)
+    w_q, s, b = oracle.quantize(w, 64, 4, out_dtype="bf16")
+    codes = oracle.unpack(w_q, 4)[0]
+    assert codes[0] == 0 and codes[1] == 8 and np.all(codes[2:] == 15)
+    assert s.tolist() == [[0xBD89]] and b.tolist() == [[0x3F80]]
+
+
 @pytest.mark.parametrize("gs", [32, 64, 128])
 @pytest.mark.parametrize("out_dtype", ["bf16", "f16", "f32"])
 def test_quantize_reconstruction_bound(gs, out_dtype):
@@ -220,6 +243,23 @@ def test_softcap_identity_and_bound():
     out = oracle.bf16_bits_to_f32(oracle.logit_softcap(v, 30.0))
     assert np.all(np.abs(out) <= 30.0) and out[2] == 0.0
     assert abs(out[3] - 2.0) < 0.02  # tanh(x) ~ x for small x
+
+
+def test_softcap_rounds_every_step_known_answer():
+    """engine/target_gemma4.py:33-40 in bf16, one op and one rounding at a
+    time, worked by hand for l = 6.34375, cap = 30 (both exact in bf16):
+      l / cap = 0.2114583 -> bf16 (step 2^-10 in [1/8, 1/4)) 217 * 2^-10 =
+        0.2119140625;
+      tanh(0.2119140625) = 0.2087978 -> 213.81 steps -> 214 * 2^-10 =
+        0.208984375;
+      0.208984375 * 30 = 6.26953125 -> bf16 (step 2^-5 in [4, 8)) 200.625
+        steps -> 201 * 2^-5 = 6.28125 (bits 0x40C9).
+    Without the first rounding: tanh(0.2114583) = 0.2083619 -> 213 steps ->
+    * 30 = 6.2402 -> 6.25; without the second: 0.2087978 * 30 = 6.26394 ->
+    6.25; so an oracle that drops either returns 0x40C8 instead."""
+    v = oracle.f32_to_bf16_bits(np.array([6.34375, -6.34375], np.float32))
+    out = oracle.logit_softcap(v, 30.0, dtype="bf16")
+    assert out.tolist() == [0x40C9, 0xC0C9]
 
 
 def test_reference_shape_generator():

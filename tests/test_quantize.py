@@ -40,9 +40,11 @@ def test_quantize_matches_oracle_bitwise(bits, gs, std):
 @pytest.mark.parametrize("bits", [4, 8])
 def test_quantize_reconstruction_bounds(bits):
     """Each weight is within half a quantisation step of its reconstruction,
-    plus what the bf16 rounding of scale and bias can move the ends of the
-    representable range (codes are clipped to it), codes stay in range, and
-    dequantize is the affine map of the codes."""
+    plus what the bf16 storage of scale and bias moves it (the codes are
+    taken against the float32 values, MLX's order: code q moves by at most
+    q * 2^-9 steps, the bias by 2^-9 |bias|), and at most one step at the
+    clipped ends; codes stay in range, and dequantize is the affine map of
+    the codes."""
     rng = np.random.default_rng(bits)
     w = torch.from_numpy((rng.standard_normal((64, 256)) * 0.05).astype(np.float32))
     q, s, b = quantize(w, 64, bits, torch.bfloat16)
@@ -51,13 +53,14 @@ def test_quantize_reconstruction_bounds(bits):
     rec = dequantize(q, s, b, 64, bits)
     step = s.float().abs().repeat_interleave(64, dim=-1)
     err = (rec - w).abs()
-    # bf16 storage of scale / bias moves a code's value by at most 2^-8 of
-    # the code range in steps; interior codes are half a step from w on top
+    # bf16 storage of scale / bias: at most 2^-9 relative each (2^-8 taken)
+    cf = torch.from_numpy(codes.astype(np.float32))
+    storage = 2.0 ** -8 * (cf * step + b.float().abs().repeat_interleave(64, dim=-1))
     slack = 2.0 ** -8 * (1 << bits)
     interior = torch.from_numpy((codes > 0) & (codes < (1 << bits) - 1))
-    assert bool((err[interior] <= 0.5 * step[interior] * (1 + 2.0 ** -8 * 16) + 1e-7).all())
+    assert bool((err[interior] <= 0.5 * step[interior] + storage[interior] + 1e-7).all())
     # the snapped scale can clip the far end of the range by one step
-    assert bool((err <= step * (1.0 + slack) + 1e-7).all())
+    assert bool((err <= step * (1.0 + slack) + storage + 1e-7).all())
     by_hand = torch.from_numpy(codes.astype(np.float32)) * s.float().repeat_interleave(64, -1) \
         + b.float().repeat_interleave(64, -1)
     assert torch.equal(rec, by_hand)

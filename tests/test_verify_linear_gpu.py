@@ -201,7 +201,7 @@ def _layer(dev, K, Nq, Nkv, Ni, seed, bias=False):
 @pytest.mark.parametrize("M", [16, 4])
 @pytest.mark.parametrize("bias", [False, True])
 def test_fused_siblings(dev, monkeypatch, M, bias):
-    """install_verify_linears(fuse_siblings=True): q/k/v and gate/up each run
+    """install_verify_linears (fuse_siblings, the default): q/k/v and gate/up each run
     as one shared-activation launch in the model's own call order; every
     member's output equals quantized_matmul_multi's for it (+ bias) bit for
     bit, whatever order the members are called in, and is within 1e-2 of the
@@ -215,8 +215,8 @@ def test_fused_siblings(dev, monkeypatch, M, bias):
     K = 2048
     fused = _layer(dev, K, 2048, 512, 4096, seed=11, bias=bias)
     plain = _layer(dev, K, 2048, 512, 4096, seed=11, bias=bias)
-    assert install_verify_linears(fused, fuse_siblings=True) == 5
-    assert install_verify_linears(plain) == 5
+    assert install_verify_linears(fused) == 5  # grouped by default
+    assert install_verify_linears(plain, fuse_siblings=False) == 5
     x = _x(dev, M, K, seed=12, scale=1.0)
     for parent, names in ((fused.self_attn, ("q_proj", "k_proj", "v_proj")),
                           (fused.mlp, ("gate_proj", "up_proj"))):
@@ -280,3 +280,141 @@ def test_fused_siblings_graph_replay(dev, monkeypatch):
             assert torch.equal(o, e)
         fwd()  # eager work between replays
         torch.cuda.synchronize()
+
+
+def _multi_of(mods, x, active=None):
+    from dflash_mlx_amd.verify_qmm import quantized_matmul_multi
+
+    idx = list(range(len(mods))) if active is None else list(active)
+    ys = quantized_matmul_multi(x, [(mods[i].weight, mods[i].scales, mods[i].biases)
+                                    for i in idx], group_size=64, bits=4)
+    return dict(zip(idx, ys))
+
+
+def test_siblings_hold_their_input(dev, monkeypatch):
+    """A group keeps the input of a launch whose outputs are not all taken,
+    so a freed input's storage cannot pass to a new tensor that the group
+    would take for it (the new tensor gets its own product); an in-place
+    update of the input (a version bump) launches again."""
+    import torch
+
+    from dflash_mlx_amd.verify_linear import install_verify_linears, prewarm_verify_kernels
+
+    monkeypatch.setenv("DFLASH_VERIFY_QMM", "1")
+    K = 2048
+    model = _layer(dev, K, 2048, 512, 4096, seed=31)
+    install_verify_linears(model)
+    prewarm_verify_kernels(model)
+    a = model.self_attn
+    mods = [a.q_proj, a.k_proj, a.v_proj]
+    x1 = _x(dev, 16, K, seed=32, scale=1.0)
+    a.q_proj(x1)
+    p1 = x1.data_ptr()
+    del x1  # k and v have not taken theirs: the group still holds x1
+    x2 = torch.empty((16, K), dtype=torch.bfloat16, device=dev)
+    assert x2.data_ptr() != p1
+    x2.copy_(_x(dev, 16, K, seed=33, scale=1.0))
+    got = {1: a.k_proj(x2), 2: a.v_proj(x2), 0: a.q_proj(x2)}
+    want = _multi_of(mods, x2)
+    for i in range(3):
+        assert torch.equal(got[i], want[i])
+    x3 = _x(dev, 16, K, seed=34, scale=1.0)
+    a.q_proj(x3)
+    x3.mul_(2.0)
+    k3 = a.k_proj(x3)
+    assert torch.equal(k3, _multi_of(mods, x3)[1])
+
+
+def test_siblings_after_prewarm_in_any_order(dev, monkeypatch):
+    """After prewarm (which warms the group and leaves nothing pending),
+    up_proj called before gate_proj on a fresh (1, 16, K) input returns the
+    shared launch's products, within 1e-2 of the ungrouped modules."""
+    import torch
+
+    from dflash_mlx_amd.verify_linear import install_verify_linears, prewarm_verify_kernels
+
+    monkeypatch.setenv("DFLASH_VERIFY_QMM", "1")
+    K = 2048
+    grouped = _layer(dev, K, 2048, 512, 4096, seed=41)
+    plain = _layer(dev, K, 2048, 512, 4096, seed=41)
+    install_verify_linears(grouped)
+    install_verify_linears(plain, fuse_siblings=False)
+    prewarm_verify_kernels(grouped)
+    x = _x(dev, 16, K, seed=42, scale=1.0).reshape(1, 16, K)
+    up = grouped.mlp.up_proj(x)
+    gate = grouped.mlp.gate_proj(x)
+    want = _multi_of([grouped.mlp.gate_proj, grouped.mlp.up_proj], x)
+    assert torch.equal(gate, want[0]) and torch.equal(up, want[1])
+    for got, ref in ((gate, plain.mlp.gate_proj(x)), (up, plain.mlp.up_proj(x))):
+        rel = float((got.float() - ref.float()).abs().max() / (ref.float().abs().max() + 1e-3))
+        assert rel <= REL_TOL
+
+
+@pytest.mark.parametrize("called", [(0,), (0, 1)])
+def test_siblings_drop_members_never_called(dev, monkeypatch, called):
+    """A layer that calls only q_proj (a shared-KV attention layer) or q and k
+    (keys used as values): the uncalled members leave the shared launch after
+    two launches whose outputs they did not take; every output is the shared
+    launch's product over the members active at that call (or, with one
+    member left, the member's own verify_matmul), bit for bit."""
+    import torch
+
+    from dflash_mlx_amd.verify_linear import install_verify_linears, prewarm_verify_kernels
+    from dflash_mlx_amd.verify_qmm import verify_matmul
+
+    monkeypatch.setenv("DFLASH_VERIFY_QMM", "1")
+    K = 2048
+    model = _layer(dev, K, 2048, 512, 4096, seed=51)
+    install_verify_linears(model)
+    prewarm_verify_kernels(model)
+    a = model.self_attn
+    mods = [a.q_proj, a.k_proj, a.v_proj]
+    grp = a.q_proj._verify_state.group
+    assert grp.active == (0, 1, 2)
+    for cycle in range(4):
+        x = _x(dev, 16, K, seed=60 + cycle, scale=1.0)
+        got = {i: mods[i](x) for i in called}
+        act = grp.active
+        if len(act) >= 2:
+            want = _multi_of(mods, x, act)
+        else:
+            want = {i: verify_matmul(x, mods[i].weight, mods[i].scales, mods[i].biases,
+                                     group_size=64, bits=4) for i in called}
+        for i in called:
+            assert torch.equal(got[i], want[i]), (cycle, i, act)
+    assert grp.active == (called if len(called) >= 2 else ())
+    # a dropped member still answers when called, with its own launch
+    x = _x(dev, 16, K, seed=70, scale=1.0)
+    v = a.v_proj(x)
+    assert torch.equal(v, verify_matmul(x, a.v_proj.weight, a.v_proj.scales, a.v_proj.biases,
+                                        group_size=64, bits=4))
+
+
+def test_siblings_share_one_pair_table(dev, monkeypatch):
+    """Grouped members keep one combined (scale, bias) pair table: each
+    member's table is a column slice of it (no per-member copy), and a
+    member's own launch over its slice equals its launch over a table of its
+    own."""
+    import torch
+
+    from dflash_mlx_amd import _runtime
+    from dflash_mlx_amd.verify_linear import install_verify_linears
+    from dflash_mlx_amd.verify_qmm import qmm_launch
+
+    monkeypatch.setenv("DFLASH_VERIFY_QMM", "1")
+    K = 2048
+    model = _layer(dev, K, 2048, 512, 4096, seed=81)
+    install_verify_linears(model)
+    for parent, names in ((model.self_attn, ("q_proj", "k_proj", "v_proj")),
+                          (model.mlp, ("gate_proj", "up_proj"))):
+        states = [getattr(parent, n)._verify_state for n in names]
+        fused = states[0].group.fused
+        assert fused is not None and fused.shape[1] == sum(q.N for q in states)
+        for q in states:
+            assert q.pairs.untyped_storage().data_ptr() == fused.untyped_storage().data_ptr()
+            assert q.stride == fused.shape[1]
+            x = _x(dev, 4, K, seed=q.N, scale=1.0)
+            own = qmm_launch(x, q.w, q.s, q.b, q.N, 64, 4,
+                             pairs=_runtime.build_sb_pairs(q.s, q.b))
+            st = torch.cuda.current_stream(dev).cuda_stream
+            assert torch.equal(q.launch(x, 4, st), own)
