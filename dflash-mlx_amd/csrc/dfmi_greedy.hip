@@ -513,8 +513,12 @@ extern "C" int dfmi_lmhead_greedy_accept_pairs(
   const int mt = M <= 16 ? 1 : 2;
   hipStream_t st = static_cast<hipStream_t>(stream);
   // with the pair table: the pair-streaming loop, 128 vocabulary rows per
-  // workgroup (the same logits, summed in the same order, as the window loop)
-  if (sb_pairs && M <= 16 && group_size >= 64 && stream_eligible(M, K, V, group_size)) {
+  // workgroup (the same logits, summed in the same order, as the window loop
+  // below); only where that window loop takes the shape too (K / group_size
+  // within one scale window), so that the logits never depend on whether a
+  // table was given
+  if (sb_pairs && M <= 16 && group_size >= 64 && stream_eligible(M, K, V, group_size) &&
+      K / group_size <= sb_max_groups(kSbPieces)) {
     a.n_blocks = (int)((V + 2 * kStreamRows - 1) / (2 * kStreamRows));
     if (h_dtype == DFMI_BF16) launch_lm_pairs<BF16>(group_size, a.n_blocks, st, a);
     else launch_lm_pairs<F16>(group_size, a.n_blocks, st, a);

@@ -404,9 +404,10 @@ size_t dfmi_lmhead_workspace_bytes(int64_t M);
 /*
  * dfmi_lmhead_greedy_accept with the lm_head's pair table (sb_pairs
  * [K/group_size][V], see dfmi_sb_pairs; 16-byte aligned; may be NULL): with
- * it, M <= 16 and gs 64 / 128 sweep the vocabulary in 128-row blocks on the
- * pair-streaming loop.  Same call sites replaced; identical outputs (the
- * same logits, summed in the same order).
+ * it, M <= 16, gs 64 / 128 and K / group_size <= 120 sweep the vocabulary in
+ * 128-row blocks on the pair-streaming loop.  Same call sites replaced;
+ * identical outputs (the same logits, summed in the same order) for every
+ * shape, with or without the table.
  */
 int dfmi_lmhead_greedy_accept_pairs(const void *h, int h_dtype, const uint32_t *w_q,
                                     const void *scales, const void *biases,

@@ -271,11 +271,14 @@ def _lmhead(dev, ht, wt, st, bt, pt, ids, M, K, V, gs):
 
 
 @pytest.mark.parametrize("M,K,V,gs", [(16, 5120, 20000, 64), (15, 2048, 32000, 128),
-                                      (16, 4096, 40000, 64), (1, 1024, 1000, 64)])
+                                      (16, 4096, 40000, 64), (1, 1024, 1000, 64),
+                                      (16, 8192, 6000, 64)])
 def test_lmhead_pairs_identical(dev, M, K, V, gs):
     """The lm_head's pair-streaming sweep (128 vocabulary rows per
     workgroup) gives the window loop's logits bit for bit, hence the same
-    tokens, accept length and bonus."""
+    tokens, accept length and bonus; a shape past one scale window (K = 8192
+    at gs 64: 128 groups) takes the same general loop with or without the
+    table."""
     import torch
 
     host, (ht, wt, st, bt) = _case(dev, M, K, V, gs, "bf16", seed=V + M)
