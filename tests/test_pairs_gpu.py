@@ -247,8 +247,9 @@ def test_functional_cache_and_module_tables(dev):
     assert not torch.equal(y0, y1)
 
 
-def _lmhead(dev, ht, wt, st, bt, pt, ids, M, K, V, gs):
-    """One dfmi_lmhead_greedy_accept_pairs call with logits out."""
+def _lmhead(dev, ht, wt, st, bt, pt, ids, M, K, V, gs, want_logits=True):
+    """One dfmi_lmhead_greedy_accept_pairs call (with logits out unless
+    want_logits is False)."""
     import torch
 
     from dflash_mlx_amd import _runtime
@@ -263,8 +264,8 @@ def _lmhead(dev, ht, wt, st, bt, pt, ids, M, K, V, gs):
     rc = lib.dfmi_lmhead_greedy_accept_pairs(
         ht.data_ptr(), _runtime.dtype_code(ht.dtype), wt.data_ptr(), st.data_ptr(), bt.data_ptr(),
         pt.data_ptr() if pt is not None else 0, 0, 0.0, ids.data_ptr(), M, K, V, gs, 4,
-        post.data_ptr(), acc.data_ptr(), bonus.data_ptr(), logits.data_ptr(), ws, wsb,
-        _runtime.stream_ptr(dev))
+        post.data_ptr(), acc.data_ptr(), bonus.data_ptr(),
+        logits.data_ptr() if want_logits else 0, ws, wsb, _runtime.stream_ptr(dev))
     L.check(rc, "dfmi_lmhead_greedy_accept_pairs")
     torch.cuda.synchronize()
     return post.cpu().numpy(), int(acc.item()), int(bonus.item()), logits
@@ -272,13 +273,15 @@ def _lmhead(dev, ht, wt, st, bt, pt, ids, M, K, V, gs):
 
 @pytest.mark.parametrize("M,K,V,gs", [(16, 5120, 20000, 64), (15, 2048, 32000, 128),
                                       (16, 4096, 40000, 64), (1, 1024, 1000, 64),
-                                      (16, 8192, 6000, 64)])
+                                      (16, 8192, 6000, 64), (16, 5120, 151936, 64),
+                                      (7, 1024, 70037, 64), (16, 256, 3000, 128)])
 def test_lmhead_pairs_identical(dev, M, K, V, gs):
     """The lm_head's pair-streaming sweep (128 vocabulary rows per
-    workgroup) gives the window loop's logits bit for bit, hence the same
-    tokens, accept length and bonus; a shape past one scale window (K = 8192
-    at gs 64: 128 groups) takes the same general loop with or without the
-    table."""
+    workgroup; the full [16,5120]x[151936,5120] config, a ragged last block,
+    one step per block at K = 256) gives the window loop's logits bit for
+    bit, hence the same tokens, accept length and bonus, with or without the
+    logits written out; a shape past one scale window (K = 8192 at gs 64:
+    128 groups) takes the same general loop with or without the table."""
     import torch
 
     host, (ht, wt, st, bt) = _case(dev, M, K, V, gs, "bf16", seed=V + M)
@@ -293,6 +296,8 @@ def test_lmhead_pairs_identical(dev, M, K, V, gs):
     r1 = _lmhead(dev, ht, wt, st, bt, pt, ids, M, K, V, gs)
     assert np.array_equal(r0[0], r1[0]) and r0[1:3] == r1[1:3]
     assert torch.equal(r0[3].view(torch.int16), r1[3].view(torch.int16))
+    r2 = _lmhead(dev, ht, wt, st, bt, pt, ids, M, K, V, gs, want_logits=False)
+    assert np.array_equal(r1[0], r2[0]) and r1[1:3] == r2[1:3]
     if M > 4:
         assert r1[1] == 3
     # and the oracle's greedy on the kernel's own logits
