@@ -10,6 +10,11 @@
  * bf16 output rounded to nearest even -- the semantics of
  * mx.quantized_matmul on the MLX CPU stream that the reference falls back to
  * (verify_qmm.py:915-919).  OpenMP over output columns.
+ *
+ * The dot products keep LANES independent fp32 partial sums (lane l takes
+ * k = l, l + LANES, ...) that are added in lane order at the end, so the
+ * compiler vectorises the inner loop without reassociating anything, and a
+ * dequantised weight row serves four activation rows per pass.
  */
 #include <math.h>
 #include <stdint.h>
@@ -24,6 +29,27 @@ static inline float bf16_to_f32(uint16_t h) {
     float f;
     memcpy(&f, &u, 4);
     return f;
+}
+
+#define LANES 16
+#define MROWS 4
+
+/* a[r] = sum_k x_r[k] w[k] for MROWS rows x_r = x + r * K (K % LANES == 0). */
+static void dot_rows(const float *x, const float *w, int64_t K, int rows, float *a) {
+    float part[MROWS][LANES];
+    for (int r = 0; r < MROWS; ++r)
+        for (int l = 0; l < LANES; ++l) part[r][l] = 0.0f;
+    for (int64_t k = 0; k < K; k += LANES)
+        for (int r = 0; r < MROWS; ++r) {
+            if (r >= rows) break;
+            const float *xr = x + r * K + k;
+            for (int l = 0; l < LANES; ++l) part[r][l] += xr[l] * w[k + l];
+        }
+    for (int r = 0; r < rows; ++r) {
+        float t = 0.0f;
+        for (int l = 0; l < LANES; ++l) t += part[r][l];
+        a[r] = t;
+    }
 }
 
 static inline uint16_t f32_to_bf16(float f) {
@@ -70,16 +96,31 @@ int oracle_qmm_bf16(const uint16_t *x, const uint32_t *w_q, const uint16_t *scal
                 for (int64_t g = 0; g < groups; ++g) {
                     const float s = bf16_to_f32(scales[n * groups + g]);
                     const float b = bf16_to_f32(biases[n * groups + g]);
-                    for (int64_t k = g * group_size; k < (g + 1) * group_size; ++k) {
-                        const uint32_t q = (wr[k / per] >> (bits * (k % per))) & mask;
-                        wrow[k] = (float)q * s + b;
+                    if (bits == 4 && group_size % 8 == 0) {
+                        /* whole words: value i of word j at bits 4i */
+                        const uint32_t *wg = wr + g * group_size / 8;
+                        float *dst = wrow + g * group_size;
+                        for (int64_t j = 0; j < group_size / 8; ++j)
+                            for (int i = 0; i < 8; ++i)
+                                dst[8 * j + i] = (float)((wg[j] >> (4 * i)) & 15u) * s + b;
+                    } else {
+                        for (int64_t k = g * group_size; k < (g + 1) * group_size; ++k) {
+                            const uint32_t q = (wr[k / per] >> (bits * (k % per))) & mask;
+                            wrow[k] = (float)q * s + b;
+                        }
                     }
                 }
-                for (int64_t m = 0; m < M; ++m) {
-                    const float *xr = xf + m * K;
-                    float a = 0.0f;
-                    for (int64_t k = 0; k < K; ++k) a += xr[k] * wrow[k];
-                    acc[m] = a;
+                if (K % LANES == 0) {
+                    for (int64_t m = 0; m < M; m += MROWS)
+                        dot_rows(xf + m * K, wrow, K, (int)(M - m < MROWS ? M - m : MROWS),
+                                 acc + m);
+                } else {
+                    for (int64_t m = 0; m < M; ++m) {
+                        const float *xr = xf + m * K;
+                        float a = 0.0f;
+                        for (int64_t k = 0; k < K; ++k) a += xr[k] * wrow[k];
+                        acc[m] = a;
+                    }
                 }
                 for (int64_t m = 0; m < M; ++m) y[m * N + n] = f32_to_bf16(acc[m]);
             }
