@@ -65,6 +65,9 @@ _SIGNATURES = {
                                   _i64, _i64, _i64, _int, _int, _c_void_p, _size,
                                   ctypes.POINTER(QmmTuning), _c_void_p]),
     "dfmi_qmm_workspace_bytes": (_size, [_i64, _i64, _i64, _int, _int]),
+    "dfmi_qmm_general": (_int, [_c_void_p, _int, _c_void_p, _c_void_p, _c_void_p, _int, _c_void_p,
+                                _i64, _i64, _i64, _int, _int, _int, _c_void_p, _size,
+                                _c_void_p]),
     "dfmi_qmm_affine_pairs": (_int, [_c_void_p, _int, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                      _c_void_p, _i64, _i64, _i64, _int, _int, _c_void_p, _size,
                                      ctypes.POINTER(QmmTuning), _c_void_p]),

@@ -282,20 +282,73 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
                      biases: torch.Tensor, *, transpose: bool = True, group_size: int = 64,
                      bits: int = 4, mode: str = "affine", tuning=None) -> torch.Tensor:
     """The "stock" quantized matmul of this framework (the role
-    ``mx.quantized_matmul`` plays for the reference): ``x . dequant(w)^T``.
+    ``mx.quantized_matmul`` plays for the reference): ``x . dequant(w)^T``
+    (``transpose=True``, w ``[N, K*bits/32]``) or ``x . dequant(w)``
+    (``transpose=False``, w ``[K, N*bits/32]`` quantised along N).
 
-    Raises :class:`_lib.DfmiUnsupported` for what the kernels do not cover
-    (transpose=False, bits other than 4 and 8, non-affine modes, fp32
-    activations).
+    Activations and scales in bf16, f16 or f32; the result has their common
+    dtype when they share one, else float32 (MLX's promotion).  x and scales
+    of one 16-bit dtype with ``transpose=True`` take the verify kernels; the
+    other cases ``dfmi_qmm_general``'s fp32 kernels.  Raises
+    :class:`_lib.DfmiUnsupported` for bits other than 4 and 8, group sizes
+    other than 32 / 64 / 128 and non-affine modes.
     """
-    if not transpose or mode != "affine":
+    if mode != "affine":
+        raise _lib.DfmiUnsupported(_lib.DFMI_EINVAL, f"mode {mode!r} is not implemented")
+    if transpose and x.dtype in _KERNEL_DTYPES and scales.dtype == x.dtype:
+        x2, wq, s, b, M, K = _prepare(x, w, scales, biases)
+        N = int(wq.shape[0])
+        y = qmm_launch(x2, wq, s, b, N, group_size, bits, tuning)
+        return y.reshape(*x.shape[:-1], N)
+    return _general(x, w, scales, biases, transpose, int(group_size), int(bits))
+
+
+_FLOAT_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
+
+
+def _general(x, w, scales, biases, transpose: bool, group_size: int, bits: int):
+    """``dfmi_qmm_general`` on the inputs the verify kernels do not take."""
+    for t, name in ((x, "x"), (w, "w"), (scales, "scales"), (biases, "biases")):
+        _runtime.require_device(t, name)
+    if x.dtype not in _FLOAT_DTYPES or scales.dtype not in _FLOAT_DTYPES:
         raise _lib.DfmiUnsupported(_lib.DFMI_EINVAL,
-                                   "only transpose=True affine quantization is implemented")
-    if x.dtype not in _KERNEL_DTYPES:
-        raise _lib.DfmiUnsupported(_lib.DFMI_EINVAL, f"x dtype {x.dtype} unsupported")
-    x2, wq, s, b, M, K = _prepare(x, w, scales, biases)
-    N = int(wq.shape[0])
-    y = qmm_launch(x2, wq, s, b, N, group_size, bits, tuning)
+                                   f"dtypes x {x.dtype}, scales {scales.dtype} unsupported")
+    if biases is None or biases.dtype != scales.dtype:
+        raise _lib.DfmiUnsupported(_lib.DFMI_EINVAL, "biases must exist and share the scales' dtype")
+    if bits not in (4, 8):
+        raise _lib.DfmiUnsupported(_lib.DFMI_EINVAL, f"bits={bits} unsupported (4 or 8)")
+    wq = _runtime.weight_words(w)
+    if wq.dim() != 2:
+        raise ValueError(f"w must be 2-D packed words, got shape {tuple(wq.shape)}")
+    K = int(x.shape[-1])
+    M = math.prod(int(d) for d in x.shape[:-1])
+    if transpose:
+        N, kw = int(wq.shape[0]), int(wq.shape[1]) * 32 // bits
+        if kw != K:
+            raise ValueError(f"w covers K={kw}, x has K={K}")
+        groups = (N, K // group_size if group_size else 0)
+    else:
+        N = int(wq.shape[1]) * 32 // bits
+        if int(wq.shape[0]) != K:
+            raise ValueError(f"w has {int(wq.shape[0])} rows, x has K={K}")
+        groups = (K, N // group_size if group_size else 0)
+    if tuple(scales.shape) != groups or tuple(biases.shape) != groups:
+        raise ValueError(f"scales / biases must be {groups}, got {tuple(scales.shape)} / "
+                         f"{tuple(biases.shape)}")
+    x2 = _runtime.aligned_contiguous(x.reshape(M, K))
+    s, b = _runtime.aligned_contiguous(scales), _runtime.aligned_contiguous(biases)
+    ydt = x.dtype if x.dtype == scales.dtype else torch.float32
+    y = torch.empty((M, N), dtype=ydt, device=x.device)
+    lib = _lib.load()
+    need = 0
+    if transpose and x.dtype == scales.dtype and x.dtype != torch.float32:
+        need = int(lib.dfmi_qmm_workspace_bytes(M, K, N, group_size, bits))
+    ws, ws_bytes = _runtime.workspace(x.device, need) if need else (0, 0)
+    status = lib.dfmi_qmm_general(
+        x2.data_ptr(), _runtime.dtype_code(x2.dtype), wq.data_ptr(), s.data_ptr(), b.data_ptr(),
+        _runtime.dtype_code(s.dtype), y.data_ptr(), M, K, N, group_size, bits, int(bool(transpose)),
+        ws, ws_bytes, _runtime.stream_ptr(x.device))
+    _lib.check(status, "dfmi_qmm_general")
     return y.reshape(*x.shape[:-1], N)
 
 

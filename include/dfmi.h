@@ -108,6 +108,27 @@ int dfmi_qmm_affine_ex(const void *x, int x_dtype, const uint32_t *w_q, const vo
 size_t dfmi_qmm_workspace_bytes(int64_t M, int64_t K, int64_t N, int group_size, int bits);
 
 /*
+ * The whole stock quantized matmul: mx.quantized_matmul, which dflash-mlx
+ * calls for every input its verify kernels decline (verify_qmm.py:915-919,
+ * 936-938, 957-959, 984-986, 1005-1007), for 4- and 8-bit affine weights at
+ * group size 32 / 64 / 128:
+ *   transpose != 0: y[M, N] = x[M, K] . dequant(w)^T, w_q [N, K*bits/32]
+ *     (16-byte aligned), scales / biases [N, K/gs]; K % gs == 0;
+ *   transpose == 0: y[M, N] = x[M, K] . dequant(w), w_q [K, N*bits/32]
+ *     quantised along N, scales / biases [K, N/gs]; N % gs == 0, any K >= 1.
+ * x_dtype and s_dtype (scales and biases) are DFMI_BF16, DFMI_F16 or
+ * DFMI_F32; y has their common dtype when they are the same, else float32
+ * (MLX's promotion).  transpose with x and scales of one 16-bit dtype is
+ * dfmi_qmm_affine_ex (same kernels and results; workspace as
+ * dfmi_qmm_workspace_bytes reports); every other case runs fp32 VALU
+ * kernels, needs no workspace (NULL, 0) and is deterministic.
+ */
+int dfmi_qmm_general(const void *x, int x_dtype, const uint32_t *w_q, const void *scales,
+                     const void *biases, int s_dtype, void *y, int64_t M, int64_t K, int64_t N,
+                     int group_size, int bits, int transpose, void *workspace,
+                     size_t workspace_bytes, void *stream);
+
+/*
  * dfmi_qmm_affine_ex with the layer's pair table as well: sb_pairs
  * [K/group_size][N] uint32, pair[g][n] = scales[n][g] | biases[n][g] << 16
  * (built once per weight by dfmi_sb_pairs; 16-byte aligned).  Same call

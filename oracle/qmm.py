@@ -108,9 +108,18 @@ def quantized_matmul(x, w_q, scales, biases, *, transpose: bool = True,
 
     ``x`` is ``[..., K]`` in ``dtype`` storage.  Returns float64 ``[..., N]``
     when ``out_dtype`` is None, else the result rounded to ``out_dtype``.
+
+    ``transpose=False`` is ``y = x . dequant(W)`` with ``w_q [K, N*bits/32]``
+    quantised along its last axis and ``scales / biases [K, N/gs]``: the
+    other orientation of ``mx.quantized_matmul`` (called by the reference's
+    fallbacks with the caller's ``transpose``, dflash_mlx/verify_qmm.py:
+    915-919; MLX's documented contract, third-party, not vendored).
     """
     if not transpose:
-        raise NotImplementedError("the verify path only uses transpose=True")
+        xf = to_f32(x, dtype).astype(np.float64)
+        w = dequantize(w_q, scales, biases, group_size, bits, dtype)  # [K, N]
+        y = xf @ w
+        return y if out_dtype is None else round_to_dtype(y, out_dtype)
     xf = to_f32(x, dtype).astype(np.float64)
     n = w_q.shape[0]
     step = 2048  # dequantise in row blocks to bound memory on large weights

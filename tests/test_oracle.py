@@ -144,6 +144,36 @@ def test_qmm_brute_force_elementwise():
     np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
 
 
+@pytest.mark.parametrize("bits", [4, 8])
+def test_qmm_untransposed_brute_force_and_orientation(bits):
+    # transpose=False: w_q [K, N*bits/32] quantised along N (groups of gs
+    # columns of one row k), y = x . dequant(w); element by element, the code
+    # of (k, n) taken straight from its word, the scale of (k, n // gs)
+    rng = np.random.default_rng(61 + bits)
+    M, K, N, gs = 2, 5, 64, 32
+    x = oracle.round_to_dtype(rng.standard_normal((M, K)).astype(np.float32), "f32")
+    w_q, s, b = oracle.quantize((rng.standard_normal((K, N)) * 0.02).astype(np.float32), gs, bits,
+                                out_dtype="f32")
+    vpw, mask = 32 // bits, (1 << bits) - 1
+    want = np.zeros((M, N))
+    for m in range(M):
+        for n in range(N):
+            acc = 0.0
+            for k in range(K):
+                q = (int(w_q[k, n // vpw]) >> (bits * (n % vpw))) & mask
+                acc += float(x[m, k]) * (q * float(s[k, n // gs]) + float(b[k, n // gs]))
+            want[m, n] = acc
+    got = oracle.quantized_matmul(x, w_q, s, b, transpose=False, group_size=gs, bits=bits,
+                                  dtype="f32")
+    np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
+    # a one-hot activation picks row k of the dequantised [K, N] matrix
+    e = np.zeros((1, K), np.float32)
+    e[0, 3] = 1.0
+    row = oracle.quantized_matmul(e, w_q, s, b, transpose=False, group_size=gs, bits=bits,
+                                  dtype="f32")[0]
+    np.testing.assert_allclose(row, oracle.dequantize(w_q, s, b, gs, bits, "f32")[3])
+
+
 def test_qmm_bias_shift_identity():
     # Adding c to every bias adds c * sum_k x[m, k] to every output.
     rng = np.random.default_rng(7)

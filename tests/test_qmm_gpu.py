@@ -217,9 +217,11 @@ def test_unsupported_raises(dev):
     s = torch.zeros((8, 2), dtype=torch.bfloat16, device=dev)
     with pytest.raises(_lib.DfmiUnsupported):
         vq.quantized_matmul(x, w, s, s, group_size=50, bits=4)
+    # (float32 activations are computed: tests/test_general_gpu.py; 3-bit
+    # weights are not)
     xf = torch.zeros((16, 64), dtype=torch.float32, device=dev)
     with pytest.raises(_lib.DfmiUnsupported):
-        vq.quantized_matmul(xf, w[:, :8], s[:, :1], s[:, :1], group_size=64, bits=4)
+        vq.quantized_matmul(xf, w[:, :6], s[:, :1], s[:, :1], group_size=64, bits=3)
 
 
 @pytest.mark.parametrize("M,K,N,gs", [
