@@ -257,8 +257,8 @@ def _build_dispatch(obj: VerifyQuantizedLinear, *, enable_qmm: Optional[bool] = 
         if state.pairs_ok and not torch.cuda.is_current_stream_capturing():
             state.pair_table()
         object.__setattr__(obj, "_verify_state", state)
-        # the kernels read scales / biases in the activation dtype: other
-        # inputs go to the stock path, which rejects them
+        # the verify kernels read scales / biases in the activation dtype:
+        # other inputs (fp32, mixed dtypes) go to the stock path
         sdt = state.s.dtype if state.s.dtype in _KERNEL_DTYPES else None
 
         def call(x: torch.Tensor) -> torch.Tensor:

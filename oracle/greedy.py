@@ -82,7 +82,7 @@ def logit_softcap(logits, softcap, *, dtype: str = "bf16"):
     """
     if softcap is None or float(softcap) <= 0.0:
         return logits
-    cap = float(to_f32(round_to_dtype(np.float32(softcap), dtype), dtype))
+    cap = float(to_f32(round_to_dtype(np.float32(softcap), dtype), dtype).reshape(-1)[0])
     l = to_f32(logits, dtype)
     t1 = to_f32(round_to_dtype(l / np.float32(cap), dtype), dtype)
     t2 = to_f32(round_to_dtype(np.tanh(t1), dtype), dtype)
