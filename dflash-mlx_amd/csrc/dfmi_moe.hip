@@ -455,7 +455,7 @@ __global__ __launch_bounds__(512) void gather_persist_kernel(GatherArgs a) {
                                ? ((uint32_t)n * (uint32_t)(K / GS) + (uint32_t)q * 8u) * 2u
                                : kNoRow;
       const uint16_t* base = arr ? (second ? ib1 : ib0) : (second ? is1 : is0);
-      dma16(buffer_rsrc(base, sbytes), off, 0u,
+      dma16<kCpolStream>(buffer_rsrc(base, sbytes), off, 0u,
             dfmi_smem + S::SB_OFF + LY::sb_base(iunit) + arr * S::NB * S::SBP + r0 * S::SBP);
       ops += S::SB_DMA;
     }
@@ -470,7 +470,7 @@ __global__ __launch_bounds__(512) void gather_persist_kernel(GatherArgs a) {
     for (int i = 0; i < S::W_DMA; ++i) {
       const int r0 = (wave * S::W_DMA + i) * RPI;  // wave-uniform
       const uint32_t* base = r0 >= SPLIT ? iw1 : iw0;
-      dma16(buffer_rsrc(base, wbytes), L.wg[i], uoff,
+      dma16<kCpolStream>(buffer_rsrc(base, wbytes), L.wg[i], uoff,
             dfmi_smem + S::W_OFF + stage * S::WBUF + r0 * S::WROW);
     }
     ops += S::CHUNK_DMA;
@@ -835,11 +835,11 @@ __global__ __launch_bounds__(512) void moe_stream_kernel(
     for (int i = 0; i < 2; ++i) {
       const int r0 = (2 * wave + i) * 8;  // wave-uniform
       const uint32_t* base = (GLU && (r0 & 63) >= 32) ? iw1 : iw0;
-      dma16(buffer_rsrc(base, wbytes), i ? lwg1 : lwg0, (uint32_t)c * (uint32_t)S::WROW,
+      dma16<kCpolStream>(buffer_rsrc(base, wbytes), i ? lwg1 : lwg0, (uint32_t)c * (uint32_t)S::WROW,
             dfmi_smem + S::W_OFF + stage * S::WBUF + r0 * S::WROW);
     }
     if (lane < S::TLANES)
-      dma16(buffer_rsrc(it, twords * 4u), ltg, (uint32_t)c * (uint32_t)(S::GPC * 4 * NTC),
+      dma16<kCpolStream>(buffer_rsrc(it, twords * 4u), ltg, (uint32_t)c * (uint32_t)(S::GPC * 4 * NTC),
             dfmi_smem + S::T_OFF + stage * S::SBS + wave * S::TPB);
     ops += S::CHUNK_DMA;
   };
