@@ -707,7 +707,8 @@ def run_gdn(args, torch):
     us_rep = ms_rep * 1e3 / layers
     gbs = tape_bytes / (us_tape * 1e-6) / 1e9
     roofline = {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                "frac": round(gbs / HBM_PEAK_GBS, 4),
+                "traffic": measured_traffic("gdn", "gdn_kernel<4, false, 0>"),
                 "kernel": "gdn_kernel<4, false, 0>", "bytes_per_launch": tape_bytes,
                 "us_per_launch": round(us_tape, 3),
                 "replay": {"kernel": "gdn_kernel<4, true, 0>", "steps": acc + 1,
