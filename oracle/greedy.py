@@ -43,7 +43,7 @@ def greedy_tokens_with_mask(logits, suppress_token_mask=None, *, dtype: str = "b
     """
     vals = to_f32(logits, dtype).astype(np.float64)
     if suppress_token_mask is not None:
-        floor = float(to_f32(round_to_dtype(np.float32(-1e9), dtype), dtype))
+        floor = float(to_f32(round_to_dtype(np.float32(-1e9), dtype), dtype).reshape(-1)[0])
         vals = np.where(np.asarray(suppress_token_mask, dtype=bool), floor, vals)
     return _argmax_first(vals)
 
