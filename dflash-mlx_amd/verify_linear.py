@@ -12,6 +12,7 @@ verify kernels; every other M goes to the stock quantized matmul.
 from __future__ import annotations
 
 import math
+import warnings
 from typing import Callable, Optional
 
 import torch
@@ -169,6 +170,21 @@ class VerifyQuantizedLinear(QuantizedLinear):
 
 _KERNEL_DTYPES = (torch.bfloat16, torch.float16)
 
+_CAPTURE_WARNED = False
+
+
+def _warn_capture_without_table() -> None:
+    """One RuntimeWarning per process for a verify launch captured into a
+    graph before its pair table was built (the graph keeps the slower
+    table-free launch; prewarm_verify_kernels before capture avoids it)."""
+    global _CAPTURE_WARNED
+    if not _CAPTURE_WARNED:
+        _CAPTURE_WARNED = True
+        warnings.warn("a verify linear was captured into a graph before its pair table was "
+                      "built: the captured launch runs without the table (same results, "
+                      "slower); call prewarm_verify_kernels(model) before capture",
+                      RuntimeWarning, stacklevel=3)
+
 
 class _VerifyState:
     """Launch state of one verify module, built once by ``_build_dispatch``:
@@ -194,9 +210,11 @@ class _VerifyState:
     def pair_table(self):
         """The pair table (built on first use; None while a graph is being
         captured before it exists: the launch then runs without it, with the
-        same plan and bit-identical results)."""
+        same plan and bit-identical results, and a RuntimeWarning says so
+        once per process)."""
         if self.pairs is None and self.pairs_ok:
             if torch.cuda.is_current_stream_capturing():
+                _warn_capture_without_table()
                 return None
             self.pairs = _runtime.build_sb_pairs(self.s, self.b)
         return self.pairs

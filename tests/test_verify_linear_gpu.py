@@ -282,6 +282,63 @@ def test_fused_siblings_graph_replay(dev, monkeypatch):
         torch.cuda.synchronize()
 
 
+def test_capture_without_prewarm_uses_the_pair_table(dev, monkeypatch):
+    """A module captured into a graph without prewarm_verify_kernels already
+    has its pair table (built with the route at install): the capture warns
+    nothing and replays bit-identical to the eager launch.  A module whose
+    table is missing at capture (constructed under capture: forced here by
+    dropping it) warns once, and its table-free launch replays bit-identical
+    to the eager launch with the table (the same plan with or without it)."""
+    import warnings
+
+    import torch
+
+    from dflash_mlx_amd import _runtime
+    from dflash_mlx_amd import verify_linear as vl
+
+    monkeypatch.setenv("DFLASH_VERIFY_QMM", "1")
+    monkeypatch.setattr(vl, "_CAPTURE_WARNED", False)
+    K = N = 4096
+    ql = _mk_ql(dev, K, N, seed=41, std=0.02)
+    verify = vl.VerifyQuantizedLinear.from_quantized(ql)
+    state = verify._verify_state
+    assert state.pairs is not None  # built at install
+    x = _x(dev, 16, K, seed=42, scale=1.0)
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        _runtime.WORKSPACES.reserve(x.device, 16 << 20)
+    stream.synchronize()
+
+    def capture():
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            out = verify(x)
+        return graph, out
+
+    with warnings.catch_warnings():
+        warnings.simplefilter("error", RuntimeWarning)
+        g1, out1 = capture()
+    eager = verify(x)
+    torch.cuda.synchronize()
+    state.pairs = None  # as if the module had been built under capture
+    state.recs.clear()
+    with pytest.warns(RuntimeWarning, match="before its pair table"):
+        g2, out2 = capture()
+    assert state.pairs is None
+    assert torch.equal(verify(x), eager)  # rebuilds the table
+    torch.cuda.synchronize()
+    assert state.pairs is not None
+    for _ in range(3):
+        for g, out in ((g1, out1), (g2, out2)):
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, eager)
+            verify(x)
+            torch.cuda.synchronize()
+    assert torch.equal(eager, _direct(ql, x))
+    _oracle_check(ql, x, eager)
+
+
 def _multi_of(mods, x, active=None):
     from dflash_mlx_amd.verify_qmm import quantized_matmul_multi
 
