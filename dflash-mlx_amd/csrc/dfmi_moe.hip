@@ -747,13 +747,19 @@ __global__ __launch_bounds__(512) void moe_stream_kernel(
   // its piece (CU h < r SP): taken by the slot with fewer whole units
   const bool has_piece = SP > 1 && h < r * SP && sh == (R & 1);
   const int PC = C / SP;
-  const int nW = n_whole * C;                // steps of the whole units
-  const int V = nW + (has_piece ? PC : 0);  // this workgroup's steps
-  if (V == 0) return;                        // uniform
+  // The piece's steps come first, then the whole units': its exchange then
+  // overlaps the CU's streaming instead of ending the launch (the lighter
+  // slot's stall there lets the other slot stream faster).
+  const int PF = has_piece ? PC : 0;     // steps of the piece
+  const int V = PF + n_whole * C;        // this workgroup's steps
+  if (V == 0) return;                    // uniform
   const int tu = h / SP, ppart = h - tu * SP;  // the piece: tail unit, part
-  auto unit_of = [&](int v) __attribute__((always_inline)) {  // unit of step v
-    return v < nW ? h + H * (2 * (v / C) + sh) : whole + tu;
-  };
+  // Positions carried across the loop (uniform, no divisions per step): the
+  // issue side runs the pipeline depth ahead of the compute side.
+  int is_next = 0, is_c = 0, is_q = 0;    // issue: next unit start, k step, whole units begun
+  int cs_next = 0;                        // compute: next unit start
+  int ce_next = PF > 0 ? PF - 1 : C - 1;  // compute: next unit end
+  int ep_q = 0;                           // epilogue: whole units finished
 
   const uint32_t wbytes = (uint32_t)N * (uint32_t)(K / 2);
   const uint32_t wwords = wbytes / 4;
@@ -789,10 +795,17 @@ __global__ __launch_bounds__(512) void moe_stream_kernel(
 
   // Issue step vi: a unit's first step sets the unit's lane offsets.
   auto issue = [&](int vi) __attribute__((always_inline)) {
-    const int c = __builtin_amdgcn_readfirstlane(vi < nW ? vi % C : ppart * PC + (vi - nW));
+    const bool first = vi == is_next;  // a unit's (or the piece's) first step
+    if (first) {
+      is_c = vi < PF ? ppart * PC : 0;
+      is_next = vi < PF ? PF : vi + C;
+    }
+    const int c = __builtin_amdgcn_readfirstlane(is_c);
+    ++is_c;
     const int stage = __builtin_amdgcn_readfirstlane(vi % kPersistStages);
-    if (vi % C == 0) {  // a unit's (or the piece's) first step
-      const int u = __builtin_amdgcn_readfirstlane(unit_of(vi));
+    if (first) {
+      const int u = __builtin_amdgcn_readfirstlane(vi < PF ? whole + tu
+                                                           : h + H * (2 * is_q++ + sh));
       const int sidx = u / ncb;
       const int cb = u - sidx * ncb;
       const int p0 = __builtin_amdgcn_readfirstlane((int)t_seg[sidx]);
@@ -864,10 +877,11 @@ __global__ __launch_bounds__(512) void moe_stream_kernel(
   // Outputs of the unit that ends at step v (the stage of the step after it
   // is free: its fragments are in registers and its next DMA follows the
   // next barrier).  A piece instead publishes its partial tiles; the last
-  // piece of a unit to arrive sums all of them in part order and finishes.
+  // piece of a unit to arrive sums all of them in part order and finishes
+  // (the others return from here and go on to their whole units).
   auto epilogue = [&](int v, int slot) __attribute__((always_inline)) {
-    const bool piece = v >= nW;  // uniform: the workgroup's last work item
-    const int u = __builtin_amdgcn_readfirstlane(unit_of(v));
+    const bool piece = v < PF;  // uniform: the workgroup's first work item
+    const int u = __builtin_amdgcn_readfirstlane(piece ? whole + tu : h + H * (2 * ep_q++ + sh));
     const int sidx = u / ncb;
     const int cb = u - sidx * ncb;
     const int p0 = __builtin_amdgcn_readfirstlane((int)t_seg[sidx]);
@@ -929,7 +943,9 @@ __global__ __launch_bounds__(512) void moe_stream_kernel(
                                __HIP_MEMORY_SCOPE_AGENT);
         }
       }
-      stage_barrier<0>();  // every partial store of the workgroup has completed
+      // every partial store of the workgroup has completed (and the next
+      // steps' DMAs in flight have landed: stores and loads share vmcnt)
+      stage_barrier<0>();
       if (tid == 0) {
         const unsigned prev =
             __hip_atomic_fetch_add(&wsc[tu], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -989,12 +1005,15 @@ __global__ __launch_bounds__(512) void moe_stream_kernel(
       if ((v) + kPersistStages < V) issue((v) + kPersistStages);              \
       read((v) + 1, NXT);                                                     \
     }                                                                         \
-    if ((v) % C == 0) {                                                       \
+    if ((v) == cs_next) {                                                     \
       _Pragma("unroll") for (int t = 0; t < S::NT; ++t) acc[t][0] = zero4(); \
+      cs_next = (v) < PF ? PF : (v) + C;                                      \
     }                                                                         \
     S::compute(L, CUR, acc, dq, ones);                                        \
-    if ((v) % C == C - 1 || (v) == V - 1)                                      \
+    if ((v) == ce_next || (v) == V - 1) {                                     \
       epilogue((v), ((v) + 1) % kPersistStages);                              \
+      ce_next += C;                                                           \
+    }                                                                         \
   } while (0)
   int v = 0;
   for (; v + 1 < V; v += 2) {
