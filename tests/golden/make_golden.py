@@ -50,7 +50,7 @@ def main():
         "random_shapes": random_shapes(),
         # tests/test_verify_qmm_parity.py:77-81, 96-100 (bf16 abs, fp16 abs, rel)
         "reference_tolerances": {"bf16_abs": 8e-3, "f16_abs": 4e-3, "rel": 2e-2},
-        # Default-env M=16 / M=4 kernel per BASELINE shape: dflash_mlx/verify_qmm.py:21-51,
+        # Default-env M=16 / M=4 kernel per 9B / 27B layer shape: dflash_mlx/verify_qmm.py:21-51,
         # verify_linear.py:141-211 -> [K, N, m16_variant, m4_kparts]
         "dispatch_table": [
             [4096, 4096, "combo_ktmpl", 2], [4096, 1024, "combo_ktmpl", 4],

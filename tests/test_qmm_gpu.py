@@ -59,7 +59,7 @@ def test_config1_single_call(dev):
 
 @pytest.mark.parametrize("K,N", [(4096, 4096), (4096, 1024), (4096, 12288), (12288, 4096),
                                  (5120, 5120), (5120, 1024), (5120, 17408), (17408, 5120)])
-def test_baseline_layer_shapes_m16(dev, K, N):
+def test_9b_27b_layer_shapes_m16(dev, K, N):
     x, w_q, s, b = make_qmm_case(16, K, N, 64, seed=K + N)
     _check(_run(dev, x, w_q, s, b, 64), x, w_q, s, b, 64)
 
