@@ -731,12 +731,14 @@ __global__ __launch_bounds__(512) void moe_stream_kernel(
   // are cut along K into SP pieces of PC = C / SP steps, one piece per CU, so
   // every CU streams R units plus at most one piece; the pieces' partial
   // tiles meet in the workspace and the last one to arrive finishes the unit.
-  // Only with a workspace and >= 4 steps per unit (a piece saves more than
-  // its exchange costs).
+  // Only with a workspace; pieces of >= 2 steps where units have >= 4 (1-step
+  // pieces there cost more in exchanges than they save), of 1 step for
+  // 2-step units (measured on the 40-layer sweep: SwiGLU units of 8 steps,
+  // down units of 2).
   const int R = units / H, r = units - R * H;
   int SP = 1;
-  if (wsc && r > 0 && C >= 4) {
-    SP = min(H / r, C / 2);
+  if (wsc && r > 0 && C >= 2) {
+    SP = min(H / r, C >= 4 ? C / 2 : C);
     while (SP > 1 && C % SP) --SP;
   }
   SP = __builtin_amdgcn_readfirstlane(SP);

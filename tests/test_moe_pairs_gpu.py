@@ -193,7 +193,8 @@ def test_gather_pairs_explicit_table_and_cache(dev):
 
 
 @pytest.mark.parametrize("glu,E,K,N", [(True, 16, 2048, 256), (False, 16, 2048, 128),
-                                       (False, 12, 1024, 256), (True, 256, 2048, 512)])
+                                       (False, 12, 1024, 256), (True, 256, 2048, 512),
+                                       (False, 256, 512, 2048)])
 def test_gather_pairs_tail_split(dev, glu, E, K, N):
     """Shapes whose last partial round of units is split along K (16 tokens
     top-8: every expert's run is one unit per column block): results match
