@@ -435,6 +435,8 @@ class SiblingGroup:
             else:
                 rec = LaunchRecord(m, first.K, x.dtype, x.device,
                                    [(q.w, q.s, q.b) for q in sts], first.gs, first.bits)
+                if any(q.pairs_ok and t is None for q, t in zip(sts, tabs)):
+                    return rec  # made while a table is still missing: not kept
             self._recs[key] = rec
         return rec
 
